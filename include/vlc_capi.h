@@ -1,0 +1,144 @@
+/*
+ * vlc_capi.h -- C ABI of the gfx950 warm partial-recompute prefill kernels.
+ *
+ * Every entry point takes plain pointers and sizes.  Device pointers are HIP
+ * device addresses; `stream` is a hipStream_t (NULL = the null stream).  No
+ * entry point allocates device memory, synchronises the host with the device,
+ * or keeps mutable global state: work is enqueued on `stream` and the caller
+ * owns every buffer (inputs, outputs and workspace).
+ *
+ * Return value: VLC_OK (0) on success, a negative VLC_ERR_* for an argument
+ * the kernels do not accept (mirroring the asserts of the reference's
+ * store_kvcache, layers/attention.py:36-39), or a positive hipError_t when a
+ * launch fails.  vlc_status_string() names a status.
+ *
+ * Element type: bf16 (2-byte elements) for attention and re-rotation; the KV
+ * scatter is a bit copy and also accepts 4-byte elements.
+ */
+#ifndef VLC_CAPI_H
+#define VLC_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VLC_ABI_VERSION 1
+
+#define VLC_OK 0
+#define VLC_ERR_INVALID (-1)     /* null pointer, bad size, stride or alignment */
+#define VLC_ERR_UNSUPPORTED (-2) /* a shape the kernels do not implement (e.g. head_dim != 128) */
+#define VLC_ERR_WORKSPACE (-3)   /* workspace smaller than the plan requires */
+#define VLC_ERR_CAPACITY (-4)    /* host plan buffer too small */
+#define VLC_ERR_PLAN (-5)        /* plan does not match the call's shapes */
+
+const char* vlc_status_string(int status);
+int vlc_abi_version(void);
+
+/*
+ * Paged KV-cache scatter of freshly computed tokens.
+ * Replaces store_kvcache / store_kvcache_kernel (layers/attention.py:10-40).
+ *
+ * For every token n in [0, num_tokens): slot = slot_mapping[n]; if slot < 0 the
+ * token is skipped (the reference skips slot == -1, layers/attention.py:23);
+ * a slot >= num_slots (rows in each cache) is skipped as well instead of being
+ * written out of bounds.  Otherwise row_elems elements of key row n and value row n are copied bit for
+ * bit to row `slot` of k_cache and v_cache (cache rows are contiguous, row
+ * stride row_elems).  key/value rows are row_elems contiguous elements at row
+ * strides key_row_stride / value_row_stride (elements): the value view that
+ * the caller passes is strided (models/qwen3.py:77-80).
+ * elem_bytes is 2 (bf16/fp16) or 4.
+ */
+int vlc_store_kvcache(const void* key, int64_t key_row_stride,
+                      const void* value, int64_t value_row_stride,
+                      void* k_cache, void* v_cache,
+                      int64_t num_slots, const int32_t* slot_mapping, int64_t num_tokens,
+                      int64_t row_elems, int elem_bytes, void* stream);
+
+/*
+ * All-layer copy of reused image KV with M-RoPE re-rotation of K.
+ * Replaces ModelRunner.copy_image_kv (engine/model_runner.py:170-180), which
+ * copies flat[:, :, new_slots] = flat[:, :, old_slots] on the cache viewed as
+ * [2, L, num_slots, Hkv*hd]; this entry point additionally rotates K by the
+ * position delta of the token's image.
+ *
+ * kv_cache: bf16, plane 0 = K, plane 1 = V; element (plane, layer, slot, head, d)
+ *   is at plane*plane_stride + layer*layer_stride + slot*(num_kv_heads*head_dim)
+ *   + head*head_dim + d (strides in elements).
+ * old_slots/new_slots: device int64 [num_tokens].  The two slot sets must not
+ *   overlap except where old == new for the same token.  A token whose old or
+ *   new slot lies outside [0, num_slots) is skipped.
+ * seg_of_token: device int32 [num_tokens] segment (image) index of each token,
+ *   or NULL for "all tokens in segment 0".
+ * cos_sin: device fp32 [num_segments][head_dim/2][2] = (cos, sin) of the
+ *   rotation angle of pair i, i.e. of delta_section(i) * inv_freq[i]; pair i is
+ *   dims (i, i + head_dim/2) (rotate-half convention, layers/rotary_embedding.py:6-14).
+ *   A pair whose entry is exactly (1, 0) is copied bit for bit.
+ * rotate_k: 0 = plain copy of K and V (the reference's behaviour), 1 = rotate K.
+ */
+int vlc_rerotate_copy_kv(void* kv_cache, int64_t plane_stride, int64_t layer_stride,
+                         int num_layers,
+                         const int64_t* old_slots, const int64_t* new_slots,
+                         int64_t num_tokens, int64_t num_slots, int num_kv_heads, int head_dim,
+                         const int32_t* seg_of_token, const float* cos_sin,
+                         int num_segments, int rotate_k, void* stream);
+
+/*
+ * Host-side work planner for vlc_varlen_attn_fwd (no device calls).
+ * Replaces the scheduling that flash_attn_varlen_func performs inside the
+ * external flash-attn library for the call at layers/attention.py:67-70.
+ *
+ * cu_seqlens_q/k: HOST int32 [num_seqs + 1] (the values prepare_prefill builds,
+ *   engine/model_runner.py:197-198,256-259,284-285).
+ * num_cus: compute units to plan for (256 on MI355X; <= 0 selects 256).
+ * Writes the plan into plan[0 .. *plan_len) (int32); returns VLC_ERR_CAPACITY
+ * with *plan_len set to the required length when plan_capacity is too small.
+ * *workspace_bytes receives the device workspace the plan needs.
+ */
+int vlc_attn_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                  int num_seqs, int num_heads_q, int num_heads_kv, int head_dim,
+                  int causal, int num_cus,
+                  int32_t* plan, int64_t plan_capacity, int64_t* plan_len,
+                  int64_t* workspace_bytes);
+
+/*
+ * Varlen GQA attention over paged or contiguous K/V (bf16 in, fp32 accumulate,
+ * bf16 out).  Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q,
+ * cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
+ * block_table) at layers/attention.py:67-70.
+ *
+ * q: [total_q, num_heads_q, head_dim], row stride q_row_stride elements.
+ * Paged mode (block_table != NULL): k/v are caches [num_blocks, page_size,
+ *   num_heads_kv, head_dim]; key j of sequence b lives in row
+ *   block_table[b*bt_row_stride + j/page_size]*page_size + j%page_size;
+ *   k_row_stride/v_row_stride are elements per cache row.  A block id outside
+ *   [0, num_blocks) reads as zeros (it is never dereferenced).
+ * Contiguous mode (block_table == NULL): key j of sequence b is row
+ *   cu_seqlens_k[b] + j of k/v, at k_row_stride / v_row_stride elements.
+ * causal: row i of a sequence with lengths (sq, sk) sees keys j <= i + sk - sq
+ *   (bottom-right alignment); rows that see no key produce zeros.
+ * cu_seqlens_q/k: DEVICE int32 [num_seqs + 1].
+ * plan_host / plan_dev: the plan from vlc_attn_plan, in host memory and as a
+ *   device copy; plan_len its length.
+ * workspace: device scratch of at least the planned workspace_bytes.
+ * out: [total_q, num_heads_q, head_dim] bf16, row stride out_row_stride.
+ */
+int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride,
+                        const void* k, int64_t k_row_stride,
+                        const void* v, int64_t v_row_stride,
+                        const int32_t* block_table, int64_t bt_row_stride, int page_size,
+                        int64_t num_blocks,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                        int num_seqs, int num_heads_q, int num_heads_kv, int head_dim,
+                        float softmax_scale, int causal,
+                        const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_len,
+                        void* out, int64_t out_row_stride,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLC_CAPI_H */

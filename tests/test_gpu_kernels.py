@@ -1,0 +1,285 @@
+"""GPU parity of the three gfx950 kernels against the CPU oracle.
+
+Scatter and the K/V reuse copy are bit-exact; attention and re-rotated K are
+held to max-abs <= 2e-2 and cosine >= 0.9995 against fp32 (tests/_util.py).
+Every case prints its name before touching the GPU.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oattn
+from oracle import prefill as opre
+from oracle import rope as orope
+from oracle import scatter as oscat
+from tests._util import assert_close, bits, gen, randn_bf16, say
+from vlcache_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+# ----------------------------------------------------------------------------- scatter
+def _scatter_case(dev, n, hkv, hd, nb, bs, seed, dtype=torch.bfloat16, neg_every=7, v_row=None):
+    g = gen(seed)
+    d = hkv * hd
+    v_row = v_row or d
+    k = torch.randn(n, hkv, hd, generator=g).to(dtype)
+    vbuf = torch.randn(n, v_row, generator=g).to(dtype)
+    v = vbuf[:, v_row - d:].reshape(n, hkv, hd) if v_row == d else vbuf[:, v_row - d:].view(n, hkv, hd)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(torch.int32)
+    if neg_every:
+        slots[::neg_every] = -1
+    kc = torch.randn(nb, bs, hkv, hd, generator=g).to(dtype)  # canary contents
+    vc = torch.randn(nb, bs, hkv, hd, generator=g).to(dtype)
+    # oracle on raw bits
+    view = torch.int16 if dtype.itemsize == 2 else torch.int32
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    oscat.store_kvcache(k.view(view).numpy(), v.contiguous().view(view).numpy(), kc_ref.view(view).numpy(),
+                        vc_ref.view(view).numpy(), slots.numpy())
+    # device
+    vbuf_d = vbuf.to(dev)
+    v_d = vbuf_d[:, v_row - d:].view(n, hkv, hd)
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    kernels.store_kvcache_raw(k.to(dev), v_d, kc_d, vc_d, slots.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(kc_d.cpu().view(view), kc_ref.view(view))
+    assert torch.equal(vc_d.cpu().view(view), vc_ref.view(view))
+
+
+def test_scatter_cfg1_strided_value(dev):
+    say("scatter: 199 tokens, 2x128 bf16, value row stride 2560, slot -1 every 7th")
+    _scatter_case(dev, 199, 2, 128, 6, 256, seed=1, v_row=2560)
+
+
+def test_scatter_cfg2_shape(dev):
+    say("scatter: 1247 tokens, 2x128 bf16, value row stride 2560")
+    _scatter_case(dev, 1247, 2, 128, 84, 256, seed=2, v_row=2560, neg_every=0)
+
+
+def test_scatter_7b_rows_fp32_and_unaligned(dev):
+    say("scatter: 7B rows 4x128 bf16; fp32 rows; unaligned 3x2 bf16 rows (element path)")
+    _scatter_case(dev, 300, 4, 128, 4, 256, seed=3, v_row=28 * 128 + 2 * 512)
+    _scatter_case(dev, 64, 2, 64, 2, 256, seed=4, dtype=torch.float32)
+    _scatter_case(dev, 50, 3, 2, 2, 64, seed=5)
+
+
+def test_scatter_out_of_range_slot_skipped(dev):
+    say("scatter: slot beyond the cache is skipped, not written")
+    n, hkv, hd, nb, bs = 8, 2, 128, 1, 16
+    k = randn_bf16((n, hkv, hd), 6)
+    v = randn_bf16((n, hkv, hd), 7)
+    slots = torch.tensor([0, 1, 16, 2, 1 << 30, -1, 3, 4], dtype=torch.int32)
+    kc = torch.zeros(nb, bs, hkv, hd, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    kernels.store_kvcache_raw(k.to(dev), v.to(dev), kc_d, vc_d, slots.to(dev))
+    torch.cuda.synchronize()
+    keep = [i for i, s in enumerate(slots.tolist()) if 0 <= s < nb * bs]
+    ref = kc.view(-1, hkv, hd).clone()
+    ref[slots[keep].long()] = k[keep]
+    assert torch.equal(kc_d.cpu().view(-1, hkv, hd), ref)
+
+
+# ----------------------------------------------------------------------------- rerotate
+def _rerotate_setup(L, nb, seed, hkv=2, hd=128):
+    g = gen(seed)
+    kv = torch.randn(2, L, nb, 256, hkv, hd, generator=g).to(torch.bfloat16)
+    return kv
+
+
+def _cfg1_slots(nb_entry=6):
+    # cached entry: image at [16, 1040) in blocks 0..5; new sequence: image at [64, 1088) in blocks 11..6
+    entry_bt = list(range(nb_entry))
+    seq_bt = list(range(2 * nb_entry - 1, nb_entry - 1, -1))
+    R = opre.recompute_count(0.1, 1024)
+    old, new = opre.image_kv_copy_slots(entry_bt, 16, seq_bt, 64, 64 + 1024, R)
+    return old, new
+
+
+def test_rerotate_zero_delta_is_bit_copy(dev):
+    say("rerotate: delta 0 over 3 layers is a bit copy of K and V")
+    kv = _rerotate_setup(3, 12, seed=10)
+    old, new = _cfg1_slots()
+    ref = kv.clone()
+    oscat.copy_image_kv(ref.view(torch.int16).numpy(), old, new)
+    kv_d = kv.to(dev)
+    cs = kernels.rerotation_table([[0, 0, 0]], 128, 1e6, (16, 24, 24), device=dev)
+    kernels.rerotate_copy_kv(kv_d, torch.tensor(old, device=dev), torch.tensor(new, device=dev), cs)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(kv_d), bits(ref))
+
+
+def test_rerotate_plain_copy_matches_reference_copy(dev):
+    say("rerotate: rotate_k=False is the reference's copy_image_kv, bit for bit")
+    kv = _rerotate_setup(2, 12, seed=11)
+    old, new = _cfg1_slots()
+    ref = kv.clone()
+    oscat.copy_image_kv(ref.view(torch.int16).numpy(), old, new)
+    kv_d = kv.to(dev)
+    kernels.rerotate_copy_kv(kv_d, torch.tensor(old, device=dev), torch.tensor(new, device=dev), rotate_k=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(kv_d), bits(ref))
+
+
+def test_rerotate_cfg1_delta48(dev):
+    say("rerotate: cfg1 slots, 921 reused tokens, delta (48,48,48), 2 layers")
+    kv = _rerotate_setup(2, 12, seed=12)
+    old, new = _cfg1_slots()
+    cs = orope.rerotation_cos_sin([[48, 48, 48]], 128, 1e6, [16, 24, 24])
+    ref = kv.clone()
+    orope.rerotate_copy_kv(ref, old, new, cs)
+    kv_d = kv.to(dev)
+    kernels.rerotate_copy_kv(kv_d, torch.tensor(old, device=dev), torch.tensor(new, device=dev), cs.to(dev))
+    torch.cuda.synchronize()
+    out = kv_d.cpu()
+    # V and every untouched row: bit-exact; rotated K: the fp32 tolerance, and in practice bit-exact.
+    assert torch.equal(out[1].view(torch.int16), ref[1].view(torch.int16))
+    flat_o = out[0].view(2, -1, 2, 128)
+    flat_r = ref[0].view(2, -1, 2, 128)
+    assert_close(flat_o[:, new], flat_r[:, new], what="rerotated K")
+    mism = (flat_o.view(torch.int16) != flat_r.view(torch.int16)).sum().item()
+    print(f"rerotated K bf16 mismatches vs oracle: {mism}")
+    assert mism == 0
+
+
+def test_rerotate_segments_negative_and_sectioned_deltas(dev):
+    say("rerotate: 3 segments, deltas (-40,-40,-40), (5,17,-3), (0,0,0); 3 layers, 4 kv heads")
+    L, nb, hkv = 3, 16, 4
+    kv = _rerotate_setup(L, nb, seed=13, hkv=hkv)
+    g = gen(14)
+    perm = torch.randperm(8 * 256, generator=g)
+    old = perm[:700].tolist()
+    new = (perm[700:1400] + 8 * 256).tolist()
+    seg = torch.randint(0, 3, (700,), generator=g, dtype=torch.int32)
+    deltas = [[-40, -40, -40], [5, 17, -3], [0, 0, 0]]
+    cs = orope.rerotation_cos_sin(deltas, 128, 1e6, [16, 24, 24])
+    ref = kv.clone()
+    orope.rerotate_copy_kv(ref, old, new, cs, seg)
+    kv_d = kv.to(dev)
+    kernels.rerotate_copy_kv(kv_d, torch.tensor(old, device=dev), torch.tensor(new, device=dev), cs.to(dev),
+                             seg.to(dev))
+    torch.cuda.synchronize()
+    out = kv_d.cpu()
+    assert torch.equal(out[1].view(torch.int16), ref[1].view(torch.int16))
+    assert_close(out[0], ref[0], what="rerotated K (segments)")
+    assert (out[0].view(torch.int16) != ref[0].view(torch.int16)).sum().item() == 0
+
+
+# ----------------------------------------------------------------------------- attention
+def _paged_case(seed, hq, hkv, subseqs, page=256, extra_blocks=3, causal=True, shuffle=True):
+    """Random q and a paged cache holding each virtual sequence's keys."""
+    g = gen(seed)
+    cu_q, cu_k = [0], [0]
+    for sq, sk in subseqs:
+        cu_q.append(cu_q[-1] + sq)
+        cu_k.append(cu_k[-1] + sk)
+    nbs = [-(-sk // page) for _, sk in subseqs]
+    nb = sum(nbs) + extra_blocks
+    ids = torch.randperm(nb, generator=g).tolist() if shuffle else list(range(nb))
+    width = max(nbs) if nbs else 1
+    bt = torch.full((len(subseqs), max(width, 1)), -1, dtype=torch.int32)
+    p = 0
+    for b, n in enumerate(nbs):
+        bt[b, :n] = torch.tensor(ids[p:p + n], dtype=torch.int32)
+        p += n
+    q = torch.randn(cu_q[-1], hq, 128, generator=g).to(torch.bfloat16)
+    kc = torch.randn(nb, page, hkv, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, page, hkv, 128, generator=g).to(torch.bfloat16)
+    return q, kc, vc, bt, cu_q, cu_k
+
+
+def _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=True, num_cus=None):
+    plan = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, causal, dev, num_cus=num_cus)
+    out = kernels.varlen_attention(q.to(dev), kc.to(dev), vc.to(dev),
+                                   torch.tensor(cu_q, dtype=torch.int32, device=dev),
+                                   torch.tensor(cu_k, dtype=torch.int32, device=dev),
+                                   128 ** -0.5, causal, bt.to(dev), plan=plan)
+    torch.cuda.synchronize()
+    return out.cpu(), plan
+
+
+@pytest.mark.parametrize("num_cus", [None, 8, 4096])
+def test_attention_cfg1_paged(dev, num_cus):
+    say(f"attention: cfg1 paged (167,167),(32,1120) 16/2 heads, num_cus={num_cus}")
+    hq, hkv = 16, 2
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(20, hq, hkv, [(167, 167), (32, 1120)])
+    out, plan = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, num_cus=num_cus)
+    print(f"plan items={plan.num_items} combines={plan.num_combine}")
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
+    assert_close(out, ref, what="cfg1 attention")
+
+
+def test_attention_7b_group7_multi_run(dev):
+    say("attention: 7B heads 28/4, runs (118,118),(275,3030),(64,3200) paged")
+    hq, hkv = 28, 4
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(21, hq, hkv, [(118, 118), (275, 3030), (64, 3200)])
+    out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
+    assert_close(out, ref, what="7B attention")
+
+
+def test_attention_batched_ragged(dev):
+    say("attention: 6 ragged sequences incl. sq=1, sq=sk, long suffix; 16/2 heads")
+    subs = [(1, 1), (1, 700), (17, 17), (300, 300), (45, 2000), (129, 513)]
+    hq, hkv = 16, 2
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(22, hq, hkv, subs)
+    out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
+    assert_close(out, ref, what="ragged attention")
+
+
+def test_attention_small_pages_and_non_causal(dev):
+    say("attention: page size 16 (per-row lookup), causal and non-causal")
+    subs = [(40, 100), (7, 7), (64, 64)]
+    hq, hkv = 8, 1
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(23, hq, hkv, subs, page=16)
+    for causal in (True, False):
+        out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=causal)
+        ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), 16)
+        assert_close(out, ref, what=f"page-16 causal={causal}")
+
+
+def test_attention_rows_without_keys_are_zero(dev):
+    say("attention: causal with sk < sq: the first sq-sk rows see no key and are zero")
+    subs = [(50, 20)]
+    hq, hkv = 4, 2
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(24, hq, hkv, subs)
+    out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
+    assert torch.count_nonzero(out[:30].float()) == 0
+    assert_close(out, ref, what="sk<sq")
+
+
+def test_attention_block_permutation_bit_identical(dev):
+    say("attention: same keys under two block layouts give bit-identical output")
+    hq, hkv = 16, 2
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(25, hq, hkv, [(100, 100), (20, 900)], shuffle=False)
+    out1, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
+    perm = torch.randperm(kc.shape[0], generator=gen(26))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    kc2, vc2 = kc[perm], vc[perm]  # block i of the new cache is old block perm[i]
+    bt2 = torch.where(bt >= 0, inv[bt.clamp(min=0).long()].to(torch.int32), bt)
+    out2, _ = _run_paged(dev, q, kc2, vc2, bt2, cu_q, cu_k, hq, hkv)
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+
+
+def test_attention_contiguous_dense_strided_v(dev):
+    say("attention: contiguous mode, dense causal 1500 tokens, v strided inside qkv rows")
+    hq, hkv, n = 16, 2, 1500
+    g = gen(27)
+    qkv = torch.randn(n, (hq + 2 * hkv) * 128, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * 128].reshape(n, hq, 128).contiguous()
+    k = qkv[:, hq * 128:(hq + hkv) * 128].reshape(n, hkv, 128).contiguous()
+    cu = [0, n]
+    qkv_d = qkv.to(dev)
+    v_d = qkv_d[:, (hq + hkv) * 128:].view(n, hkv, 128)
+    plan = kernels.plan_attention(cu, cu, hq, hkv, 128, True, dev)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=dev)
+    out = kernels.varlen_attention(q.to(dev), k.to(dev), v_d, cu_d, cu_d, 128 ** -0.5, True, None, plan=plan)
+    torch.cuda.synchronize()
+    v = qkv[:, (hq + hkv) * 128:].reshape(n, hkv, 128)
+    ref = oattn.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, True, None)
+    assert_close(out.cpu(), ref, what="dense contiguous")

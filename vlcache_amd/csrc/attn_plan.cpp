@@ -1,0 +1,129 @@
+// Host-side work planner for the varlen attention kernel.
+//
+// flash-attn decides its grid from max_seqlen inside the library that the
+// reference calls (layers/attention.py:67-70); here the host, which already
+// knows every sequence length when it prepares the step
+// (engine/model_runner.py:194-320), builds an explicit work list once per step
+// and every layer reuses it:
+//   * one item per (sequence, kv head, tile of query positions); a tile holds
+//     kCols / group positions so that the group's q heads fill the MFMA columns
+//     and share every K/V tile that is staged in LDS;
+//   * the key range of an item stops at the causal limit of its last row
+//     (bottom-right alignment), so masked tiles are never visited;
+//   * items whose key range is much longer than the average are split into
+//     chunks of whole 64-key tiles (split-KV); their partial (O, m, l) go to a
+//     workspace slot and a combine pass merges them with a log-sum-exp rule;
+//   * items are ordered longest first so the dispatcher hands the long ones out
+//     before the short ones (longest-processing-time order).
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "attn_plan.h"
+#include "common_host.h"
+
+namespace {
+
+using namespace vlc::attn;
+
+struct Item {
+  int32_t v[kItemInts];
+  int64_t cost;
+};
+
+}  // namespace
+
+VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num_seqs,
+                               int num_heads_q, int num_heads_kv, int head_dim, int causal,
+                               int num_cus, int32_t* plan, int64_t plan_capacity,
+                               int64_t* plan_len, int64_t* workspace_bytes) {
+  if (!cu_q || !cu_k || !plan_len || !workspace_bytes || num_seqs < 0) return VLC_ERR_INVALID;
+  if (num_heads_q <= 0 || num_heads_kv <= 0 || num_heads_q % num_heads_kv != 0) return VLC_ERR_INVALID;
+  if (head_dim != kHeadDim) return VLC_ERR_UNSUPPORTED;
+  const int group = num_heads_q / num_heads_kv;
+  if (group > kCols) return VLC_ERR_UNSUPPORTED;
+  const int ppt = kCols / group;
+  if (num_cus <= 0) num_cus = 256;
+
+  struct Tile {
+    int b, g, qs, qc, kmax, nkt;
+  };
+  std::vector<Tile> tiles;
+  int64_t total = 0;
+  for (int b = 0; b < num_seqs; ++b) {
+    const int64_t sq = (int64_t)cu_q[b + 1] - cu_q[b];
+    const int64_t sk = (int64_t)cu_k[b + 1] - cu_k[b];
+    if (sq < 0 || sk < 0 || cu_q[b] < 0 || cu_k[b] < 0) return VLC_ERR_INVALID;
+    for (int64_t qs = 0; qs < sq; qs += ppt) {
+      const int qc = (int)std::min<int64_t>(ppt, sq - qs);
+      int64_t kmax = sk;
+      if (causal) kmax = std::max<int64_t>(0, std::min<int64_t>(sk, qs + qc + sk - sq));
+      const int nkt = (int)((kmax + kTileK - 1) / kTileK);
+      for (int g = 0; g < num_heads_kv; ++g) {
+        tiles.push_back({b, g, (int)qs, qc, (int)kmax, nkt});
+        total += std::max(nkt, 1);
+      }
+    }
+  }
+
+  // Split long key ranges so that roughly two workgroups per CU have work.
+  const int64_t target_blocks = 2LL * num_cus;
+  int64_t chunk = (total + target_blocks - 1) / std::max<int64_t>(1, target_blocks);
+  chunk = std::max<int64_t>(chunk, kMinChunkTiles);
+
+  std::vector<Item> items;
+  std::vector<Item> combines;
+  int32_t next_slot = 0;
+  items.reserve(tiles.size());
+  for (const Tile& t : tiles) {
+    // Round to the nearest number of chunks: a range up to 1.5 chunks stays whole.
+    int nsplit = (int)std::min<int64_t>(kMaxSplits, std::max<int64_t>(1, (2 * t.nkt + chunk) / (2 * chunk)));
+    if (nsplit <= 1) {
+      Item it{};
+      it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;
+      it.v[4] = 0; it.v[5] = t.kmax; it.v[6] = -1; it.v[7] = 0;
+      it.cost = std::max(t.nkt, 1);
+      items.push_back(it);
+      continue;
+    }
+    const int per = (t.nkt + nsplit - 1) / nsplit;  // key tiles per split
+    nsplit = (t.nkt + per - 1) / per;
+    Item c{};
+    c.v[0] = t.b; c.v[1] = t.g; c.v[2] = t.qs; c.v[3] = t.qc; c.v[4] = next_slot; c.v[5] = nsplit;
+    c.cost = nsplit;
+    combines.push_back(c);
+    for (int s = 0; s < nsplit; ++s) {
+      Item it{};
+      const int kb = s * per * kTileK;
+      const int ke = std::min(t.kmax, (s + 1) * per * kTileK);
+      it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;
+      it.v[4] = kb; it.v[5] = ke; it.v[6] = next_slot + s; it.v[7] = 0;
+      it.cost = (ke - kb + kTileK - 1) / kTileK;
+      items.push_back(it);
+    }
+    next_slot += nsplit;
+  }
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item& a, const Item& b) { return a.cost > b.cost; });
+
+  const int64_t need = kHeaderInts + (int64_t)(items.size() + combines.size()) * kItemInts;
+  *plan_len = need;
+  *workspace_bytes = (int64_t)next_slot * kSlotBytes;
+  if (!plan || plan_capacity < need) return VLC_ERR_CAPACITY;
+  std::memset(plan, 0, sizeof(int32_t) * kHeaderInts);
+  plan[kPMagic] = kPlanMagic;
+  plan[kPNumItems] = (int32_t)items.size();
+  plan[kPNumCombine] = (int32_t)combines.size();
+  plan[kPNumSlots] = next_slot;
+  plan[kPCols] = kCols;
+  plan[kPPositionsPerTile] = ppt;
+  plan[kPGroup] = group;
+  plan[kPNumSeqs] = num_seqs;
+  plan[kPNumHeadsKv] = num_heads_kv;
+  plan[kPCausal] = causal ? 1 : 0;
+  plan[kPHeadDim] = head_dim;
+  int32_t* w = plan + kHeaderInts;
+  for (const Item& it : items) { std::memcpy(w, it.v, sizeof(it.v)); w += kItemInts; }
+  for (const Item& c : combines) { std::memcpy(w, c.v, sizeof(c.v)); w += kItemInts; }
+  return VLC_OK;
+}

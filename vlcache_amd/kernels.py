@@ -1,0 +1,266 @@
+"""torch-facing wrappers of the gfx950 kernels (C ABI in include/vlc_capi.h).
+
+torch supplies device memory and the current stream; every computation runs in
+the HIP library.  Tensors must live on a HIP device: there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128  # the attention kernel's head dimension
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_device(name: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"{name}: tensors must be on a HIP device (got {t.device}); "
+                               "the gfx950 kernels have no CPU path")
+
+
+def _num_cus(device: torch.device) -> int:
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
+# --------------------------------------------------------------------------- scatter
+def store_kvcache_raw(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Scatter K/V rows of fresh tokens into the paged cache (vlc_store_kvcache).
+
+    key/value: [N, Hkv, hd] with contiguous rows (value may have any row stride);
+    caches: [num_blocks, block_size, Hkv, hd] contiguous rows; slot_mapping: int32 [N].
+    """
+    _require_device("store_kvcache", key, value, k_cache, v_cache, slot_mapping)
+    if slot_mapping.dtype != torch.int32:
+        raise TypeError("slot_mapping must be int32")
+    n = key.shape[0]
+    d = key.shape[1] * key.shape[2]
+    if value.shape != key.shape or slot_mapping.numel() != n:
+        raise ValueError("key, value and slot_mapping must agree in the number of tokens")
+    if key.dtype != value.dtype or k_cache.dtype != key.dtype or v_cache.dtype != key.dtype:
+        raise TypeError("key, value and the caches must share one dtype")
+    for name, t in (("key", key), ("value", value)):
+        if t.stride(-1) != 1 or t.stride(1) != key.shape[2]:
+            raise ValueError(f"{name}: each token row must be {d} contiguous elements")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache must be contiguous")
+    num_slots = k_cache.numel() // d
+    if v_cache.numel() // d != num_slots:
+        raise ValueError("k_cache and v_cache differ in size")
+    st = _lib.load().vlc_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), num_slots, slot_mapping.data_ptr(), n, d,
+        key.element_size(), _stream(key))
+    _lib.check("vlc_store_kvcache", st)
+
+
+# --------------------------------------------------------------------------- rerotate
+def rerotation_table(deltas, head_dim: int, theta: float, mrope_section=None,
+                     device=None) -> torch.Tensor:
+    """fp32 [num_segments, head_dim/2, 2] (cos, sin) of the per-pair rotation angle.
+
+    deltas: [num_segments, 3] (dt, dh, dw) position shifts, or [num_segments] for
+    a 1-D shift.  Pair i (dims i, i + hd/2) turns by delta_section(i) *
+    inv_freq[i], inv_freq[i] = theta^(-2i/hd) in fp32 as the reference's rotary
+    cache computes it (layers/rotary_embedding.py:29-33); section(i) follows
+    mrope_section (e.g. [16, 24, 24]: t for i < 16, h for i < 40, w after),
+    or the t delta for every pair when mrope_section is None.
+    """
+    d = torch.as_tensor(np.asarray(deltas), dtype=torch.float64)
+    if d.dim() == 1:
+        d = d[:, None].expand(-1, 3)
+    half = head_dim // 2
+    sec = torch.zeros(half, dtype=torch.long)
+    if mrope_section is not None:
+        if sum(mrope_section) != half:
+            raise ValueError("mrope_section must sum to head_dim / 2")
+        sec = torch.repeat_interleave(torch.arange(3), torch.as_tensor(list(mrope_section)))
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+    ang = d[:, sec].to(torch.float32) * inv[None, :]
+    tab = torch.stack((ang.cos(), ang.sin()), dim=-1).contiguous()
+    return tab if device is None else tab.to(device)
+
+
+def rerotate_copy_kv(kv_cache: torch.Tensor, old_slots: torch.Tensor, new_slots: torch.Tensor,
+                     cos_sin: torch.Tensor | None = None, seg_of_token: torch.Tensor | None = None,
+                     rotate_k: bool = True) -> None:
+    """All-layer image-KV reuse copy with K re-rotation (vlc_rerotate_copy_kv).
+
+    kv_cache: bf16 [2, L, num_blocks, block_size, Hkv, hd] (contiguous);
+    old_slots/new_slots: int64 [n] on the device; cos_sin: fp32 [nseg, hd/2, 2];
+    seg_of_token: int32 [n] or None (segment 0).  rotate_k=False is the
+    reference's plain copy.
+    """
+    _require_device("rerotate_copy_kv", kv_cache, old_slots, new_slots, cos_sin, seg_of_token)
+    if kv_cache.dtype != torch.bfloat16 or not kv_cache.is_contiguous() or kv_cache.dim() != 6:
+        raise ValueError("kv_cache must be a contiguous bf16 [2, L, blocks, block_size, Hkv, hd] tensor")
+    if old_slots.dtype != torch.int64 or new_slots.dtype != torch.int64:
+        raise TypeError("old_slots/new_slots must be int64")
+    n = old_slots.numel()
+    if new_slots.numel() != n:
+        raise ValueError("old_slots and new_slots differ in length")
+    _, L, nb, bs, hkv, hd = kv_cache.shape
+    nseg = 0
+    if rotate_k:
+        if cos_sin is None:
+            raise ValueError("rotate_k needs a cos_sin table")
+        if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.shape[1:] != (hd // 2, 2):
+            raise ValueError("cos_sin must be contiguous fp32 [num_segments, head_dim/2, 2]")
+        nseg = cos_sin.shape[0]
+    if seg_of_token is not None:
+        if seg_of_token.dtype != torch.int32 or seg_of_token.numel() != n:
+            raise ValueError("seg_of_token must be int32 [n]")
+    st = _lib.load().vlc_rerotate_copy_kv(
+        kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), L,
+        old_slots.data_ptr(), new_slots.data_ptr(), n, nb * bs, hkv, hd,
+        seg_of_token.data_ptr() if seg_of_token is not None else None,
+        cos_sin.data_ptr() if (rotate_k and cos_sin is not None) else None,
+        nseg, 1 if rotate_k else 0, _stream(kv_cache))
+    _lib.check("vlc_rerotate_copy_kv", st)
+
+
+# --------------------------------------------------------------------------- attention
+@dataclass
+class AttnPlan:
+    """A work plan for vlc_varlen_attn_fwd, built once per step and shared by every layer."""
+    host: np.ndarray           # int32 plan (kept alive: its pointer is passed to each call)
+    dev: torch.Tensor          # device copy
+    workspace: torch.Tensor | None
+    num_seqs: int
+    num_heads_q: int
+    num_heads_kv: int
+    causal: bool
+    cu_seqlens_q: tuple
+    cu_seqlens_k: tuple
+
+    @property
+    def num_items(self) -> int:
+        return int(self.host[1])
+
+    @property
+    def num_combine(self) -> int:
+        return int(self.host[2])
+
+    @property
+    def num_slots(self) -> int:
+        return int(self.host[3])
+
+
+def plan_attention(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: int,
+                   head_dim: int, causal: bool, device, num_cus: int | None = None) -> AttnPlan:
+    """Build the host work list (vlc_attn_plan) from HOST sequence boundaries."""
+    lib = _lib.load()
+    cu_q = np.ascontiguousarray(np.asarray(cu_seqlens_q, dtype=np.int32))
+    cu_k = np.ascontiguousarray(np.asarray(cu_seqlens_k, dtype=np.int32))
+    if cu_q.shape != cu_k.shape or cu_q.ndim != 1 or cu_q.size < 1:
+        raise ValueError("cu_seqlens_q/k must be 1-D and of equal length")
+    device = torch.device(device)
+    if num_cus is None:
+        num_cus = _num_cus(device) if device.type == "cuda" else 256
+    plan_len = ctypes.c_int64(0)
+    ws = ctypes.c_int64(0)
+    ip = ctypes.POINTER(ctypes.c_int32)
+    args = (cu_q.ctypes.data_as(ip), cu_k.ctypes.data_as(ip), cu_q.size - 1, num_heads_q, num_heads_kv,
+            head_dim, 1 if causal else 0, num_cus)
+    st = lib.vlc_attn_plan(*args, None, 0, ctypes.byref(plan_len), ctypes.byref(ws))
+    if st not in (0, _lib.VLC_ERR_CAPACITY):
+        _lib.check("vlc_attn_plan", st)
+    host = np.zeros(plan_len.value, dtype=np.int32)
+    st = lib.vlc_attn_plan(*args, host.ctypes.data_as(ip), host.size, ctypes.byref(plan_len),
+                           ctypes.byref(ws))
+    _lib.check("vlc_attn_plan", st)
+    if device.type == "cuda":
+        pinned = torch.from_numpy(host).pin_memory()
+        dev = pinned.to(device, non_blocking=True)
+        workspace = torch.empty(ws.value, dtype=torch.uint8, device=device) if ws.value > 0 else None
+    else:
+        dev = torch.from_numpy(host.copy())
+        workspace = None
+    return AttnPlan(host, dev, workspace, cu_q.size - 1, num_heads_q, num_heads_kv, bool(causal),
+                    tuple(int(x) for x in cu_q), tuple(int(x) for x in cu_k))
+
+
+def _check_rows(name: str, t: torch.Tensor, heads: int) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bf16")
+    if t.shape[-1] != HEAD_DIM or t.shape[-2] != heads:
+        raise ValueError(f"{name}: expected [..., {heads}, {HEAD_DIM}], got {tuple(t.shape)}")
+    if t.stride(-1) != 1 or t.stride(-2) != HEAD_DIM:
+        raise ValueError(f"{name}: heads must be contiguous rows of {HEAD_DIM} elements")
+
+
+def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, softmax_scale: float,
+                     causal: bool = True, block_table: torch.Tensor | None = None,
+                     plan: AttnPlan | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Varlen GQA attention, paged (block_table given) or contiguous (vlc_varlen_attn_fwd).
+
+    q: [total_q, Hq, 128] bf16.  Paged: k/v caches [num_blocks, page, Hkv, 128];
+    contiguous: k/v [total_k, Hkv, 128] (v may be a strided view).  cu_seqlens_*:
+    int32 device tensors.  plan: from plan_attention over the same host
+    boundaries; when None it is built here from a device-to-host copy of the
+    boundaries (a synchronisation).
+    """
+    _require_device("varlen_attention", q, k, v, cu_seqlens_q, cu_seqlens_k, block_table)
+    hq = q.shape[1]
+    paged = block_table is not None
+    hkv = k.shape[-2]
+    _check_rows("q", q, hq)
+    _check_rows("k", k, hkv)
+    _check_rows("v", v, hkv)
+    if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
+        raise TypeError("cu_seqlens must be int32")
+    num_seqs = cu_seqlens_q.numel() - 1
+    if paged:
+        if k.dim() != 4 or v.shape != k.shape:
+            raise ValueError("paged k/v must be caches [num_blocks, page, Hkv, hd]")
+        if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != num_seqs:
+            raise ValueError("block_table must be int32 [num_seqs, max_blocks]")
+        if block_table.stride(1) != 1:
+            raise ValueError("block_table rows must be contiguous")
+        k_rs, v_rs = k.stride(1), v.stride(1)
+        if k.stride(0) != k.shape[1] * k_rs or v.stride(0) != v.shape[1] * v_rs:
+            raise ValueError("paged caches must have contiguous pages")
+        page, nblocks = k.shape[1], k.shape[0]
+        bt_ptr, bt_rs = block_table.data_ptr(), block_table.stride(0)
+    else:
+        k_rs, v_rs = k.stride(0), v.stride(0)
+        page, nblocks, bt_ptr, bt_rs = 0, 0, None, 0
+    if plan is None:
+        plan = plan_attention(cu_seqlens_q.tolist(), cu_seqlens_k.tolist(), hq, hkv, HEAD_DIM, causal,
+                              q.device)
+    if plan.num_seqs != num_seqs or plan.num_heads_q != hq or plan.num_heads_kv != hkv or plan.causal != bool(causal):
+        raise ValueError("attention plan does not match the call")
+    # Bounds the kernel relies on, checked against the plan's host boundaries
+    # (the device cu_seqlens must hold the same values).
+    if plan.cu_seqlens_q[-1] > q.shape[0]:
+        raise ValueError("cu_seqlens_q exceeds the rows of q")
+    if paged:
+        max_sk = max((plan.cu_seqlens_k[i + 1] - plan.cu_seqlens_k[i] for i in range(num_seqs)), default=0)
+        if -(-max_sk // page) > block_table.shape[1]:
+            raise ValueError("block_table has fewer columns than the longest sequence needs")
+    elif plan.cu_seqlens_k[-1] > k.shape[0] or plan.cu_seqlens_k[-1] > v.shape[0]:
+        raise ValueError("cu_seqlens_k exceeds the rows of k/v")
+    if out is None:
+        out = torch.empty(q.shape[0], hq, HEAD_DIM, dtype=torch.bfloat16, device=q.device)
+    ws = plan.workspace
+    st = _lib.load().vlc_varlen_attn_fwd(
+        q.data_ptr(), q.stride(0), k.data_ptr(), k_rs, v.data_ptr(), v_rs,
+        bt_ptr, bt_rs, page, nblocks, cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+        num_seqs, hq, hkv, HEAD_DIM, float(softmax_scale), 1 if causal else 0,
+        plan.host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), plan.dev.data_ptr(), plan.host.size,
+        out.data_ptr(), out.stride(0), ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, _stream(q))
+    _lib.check("vlc_varlen_attn_fwd", st)
+    return out
