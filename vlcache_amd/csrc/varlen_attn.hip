@@ -70,16 +70,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Physical row (in elements of k/v row stride) of key `key` of sequence b; -1 if
-// the block id is outside the cache.
-__device__ __forceinline__ int64_t key_row(const Params& p, int b, int k0, int key) {
-  if (!p.block_table) return (int64_t)k0 + key;
-  const int pg = key / p.page_size;
-  const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];
-  if (blk < 0 || blk >= p.num_blocks) return -1;
-  return (int64_t)blk * p.page_size + (key - pg * p.page_size);
-}
+// How keys map to rows of k/v.
+enum KvMode {
+  kContiguous = 0,  // key j of sequence b is row cu_k[b] + j
+  kPagedTiles = 1,  // paged, page_size % 64 == 0: a 64-key tile lies inside one page
+  kPagedRows = 2,   // paged, any page size: one block-table lookup per row
+};
 
+// Online-softmax threshold (log2 units): the running max only moves when a tile's
+// max exceeds it by more than this, so P stays <= 2^8 and O is rarely rescaled.
+constexpr float kRescaleThreshold = 8.0f;
+
+template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTileK * kKS];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kHeadDim * kVS];
@@ -104,18 +106,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const bool valid = pos < q_count;
   const int qpos = q_start + pos;
   const int head = g * p.group + hh;
-  const int limit = p.causal ? qpos + sk - sq : sk - 1;               // last visible key
-  const int blk_min_limit = p.causal ? q_start + sk - sq : sk - 1;    // smallest limit in the block
+  const int limit = p.causal ? qpos + sk - sq : sk - 1;             // last visible key
+  const int blk_min_limit = p.causal ? q_start + sk - sq : sk - 1;  // smallest limit in the block
 
   // Q^T fragment (B operand of S^T = K Q^T): lane holds Q[col][16*kk + 8*hf .. +8].
+  // Invalid columns load row 0 (always readable) and are zeroed.
   bf16x8 qf[8];
   {
-    const uint16_t* qrow = p.q + (int64_t)(q0 + (valid ? qpos : 0)) * p.q_row_stride +
-                           (int64_t)head * kHeadDim + 8 * hf;
+    const uint16_t* qrow = p.q + (valid ? (int64_t)(q0 + qpos) * p.q_row_stride + (int64_t)head * kHeadDim : 0) +
+                           8 * hf;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      u32x4v w = {0u, 0u, 0u, 0u};
-      if (valid) w = *reinterpret_cast<const u32x4v*>(qrow + 16 * kk);
+      u32x4v w = *reinterpret_cast<const u32x4v*>(qrow + 16 * kk);
+      if (!valid) w = u32x4v{0u, 0u, 0u, 0u};
       qf[kk] = __builtin_bit_cast(bf16x8, w);
     }
   }
@@ -125,69 +128,137 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[mb][e] = 0.f;
-  float m = -INFINITY;
+  float mb_run = -INFINITY;  // running max, already scaled to log2 units
   float l = 0.f;
 
-  const bool one_page_tiles = p.block_table && (p.page_size % kTileK == 0);
+  // ---- K/V tile staging -------------------------------------------------------
+  // A lane moves 16 bytes of 4 K rows (r0, r0+16, r0+32, r0+48) and of 4 V rows
+  // (key pairs r0 and r0+16) per 64-key tile.  For the contiguous and the
+  // page-aligned modes a tile is 64 consecutive rows from a uniform base, so the
+  // loads are "uniform pointer + per-lane 32-bit offset" with offsets computed
+  // once; rows past sk (only in the last tile) are redirected to the tile's first
+  // row and zeroed when the tile is written to LDS.
+  const int dc = tid & 15;
+  const int r0 = tid >> 4;
+  const int64_t kst = p.k_row_stride, vst = p.v_row_stride;
+  const char* kcol = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim + dc * 8);
+  const char* vcol = reinterpret_cast<const char*>(p.v + (int64_t)g * kHeadDim + dc * 8);
+  const uint32_t ko0 = (uint32_t)(r0 * kst * 2), ko1 = (uint32_t)((r0 + 16) * kst * 2),
+                 ko2 = (uint32_t)((r0 + 32) * kst * 2), ko3 = (uint32_t)((r0 + 48) * kst * 2);
+  const uint32_t vo0 = (uint32_t)(2 * r0 * vst * 2), vo1 = (uint32_t)((2 * r0 + 1) * vst * 2),
+                 vo2 = (uint32_t)((2 * r0 + 32) * vst * 2), vo3 = (uint32_t)((2 * r0 + 33) * vst * 2);
 
-  for (int kt = k_begin; kt < k_end; kt += kTileK) {
-    __syncthreads();  // the previous tile is fully consumed
-    // ---- stage K (row-major) and V (transposed) into LDS; keys >= sk read as zeros ----
-    int64_t tile_row0 = 0;
-    bool tile_ok = true;
-    if (one_page_tiles) {
+  struct TileRegs {
+    u32x4v k0, k1, k2, k3;
+    u32x4v va0, vb0, va1, vb1;
+  };
+  auto ld16 = [](const char* base, uint32_t off) -> u32x4v {
+    return *reinterpret_cast<const u32x4v*>(base + off);
+  };
+  // Physical row of key `key` through the block table (generic page size), or -1.
+  auto paged_row = [&](int key) -> int64_t {
+    const int kc = min(key, sk - 1);
+    const int pg = kc / p.page_size;
+    const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];
+    const bool ok = key < sk && blk >= 0 && blk < p.num_blocks;
+    return ok ? (int64_t)blk * p.page_size + (kc - pg * p.page_size) : -1;
+  };
+  auto load_tile = [&](int kt) -> TileRegs {
+    TileRegs t;
+    if (MODE == kPagedRows) {
+      auto ld = [&](const char* col, int64_t st, int key) -> u32x4v {
+        const int64_t row = paged_row(key);
+        return ld16(col + (row >= 0 ? row : 0) * st * 2, 0u);
+      };
+      t.k0 = ld(kcol, kst, kt + r0);
+      t.k1 = ld(kcol, kst, kt + r0 + 16);
+      t.k2 = ld(kcol, kst, kt + r0 + 32);
+      t.k3 = ld(kcol, kst, kt + r0 + 48);
+      t.va0 = ld(vcol, vst, kt + 2 * r0);
+      t.vb0 = ld(vcol, vst, kt + 2 * r0 + 1);
+      t.va1 = ld(vcol, vst, kt + 2 * r0 + 32);
+      t.vb1 = ld(vcol, vst, kt + 2 * r0 + 33);
+      return t;
+    }
+    int64_t row0;
+    bool ok = true;
+    if (MODE == kContiguous) {
+      row0 = (int64_t)k0 + kt;
+    } else {
       const int pg = kt / p.page_size;
-      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];
-      tile_ok = blk >= 0 && blk < p.num_blocks;
-      tile_row0 = (int64_t)blk * p.page_size + (kt - pg * p.page_size);
+      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];  // uniform: scalar load
+      ok = blk >= 0 && blk < p.num_blocks;
+      row0 = ok ? (int64_t)blk * p.page_size + (kt - pg * p.page_size) : 0;
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int id = r * kThreads + tid;
-      const int row = id >> 4;
-      const int dc = id & 15;
-      const int key = kt + row;
-      u32x4v w = {0u, 0u, 0u, 0u};
-      if (key < sk) {
-        int64_t prow;
-        if (one_page_tiles) prow = tile_ok ? tile_row0 + row : -1;
-        else prow = key_row(p, b, k0, key);
-        if (prow >= 0)
-          w = *reinterpret_cast<const u32x4v*>(p.k + prow * p.k_row_stride + (int64_t)g * kHeadDim + dc * 8);
-      }
-      *reinterpret_cast<u32x4v*>(k_lds + row * kKS + dc * 8) = w;
+    const char* kb = kcol + row0 * kst * 2;
+    const char* vb = vcol + row0 * vst * 2;
+    if (ok && kt + kTileK <= sk) {
+      t.k0 = ld16(kb, ko0); t.k1 = ld16(kb, ko1); t.k2 = ld16(kb, ko2); t.k3 = ld16(kb, ko3);
+      t.va0 = ld16(vb, vo0); t.vb0 = ld16(vb, vo1); t.va1 = ld16(vb, vo2); t.vb1 = ld16(vb, vo3);
+    } else {  // last (partial) tile or a bad block id: stay inside the tile's valid rows
+      const int nvalid = ok ? sk - kt : 1;
+      auto o = [&](uint32_t off, int r) { return r < nvalid ? off : 0u; };
+      t.k0 = ld16(kb, o(ko0, r0)); t.k1 = ld16(kb, o(ko1, r0 + 16));
+      t.k2 = ld16(kb, o(ko2, r0 + 32)); t.k3 = ld16(kb, o(ko3, r0 + 48));
+      t.va0 = ld16(vb, o(vo0, 2 * r0)); t.vb0 = ld16(vb, o(vo1, 2 * r0 + 1));
+      t.va1 = ld16(vb, o(vo2, 2 * r0 + 32)); t.vb1 = ld16(vb, o(vo3, 2 * r0 + 33));
     }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int id = r * kThreads + tid;
-      const int kp = id >> 4;  // key pair 0..31
-      const int dc = id & 15;
-      u32x4v va = {0u, 0u, 0u, 0u}, vb = {0u, 0u, 0u, 0u};
-      const int key = kt + 2 * kp;
-      if (key < sk) {
-        int64_t prow;
-        if (one_page_tiles) prow = tile_ok ? tile_row0 + 2 * kp : -1;
-        else prow = key_row(p, b, k0, key);
-        if (prow >= 0)
-          va = *reinterpret_cast<const u32x4v*>(p.v + prow * p.v_row_stride + (int64_t)g * kHeadDim + dc * 8);
+    return t;
+  };
+  // Register -> LDS: K row-major, V transposed (two keys packed per 32-bit word).
+  // V rows with no valid key are zeroed here (K needs no zeroing: their scores are
+  // masked).  A tile whose block id is bad reads as all-zero V.
+  auto store_tile = [&](TileRegs t, int kt) {
+    bool clean = kt + kTileK <= sk;
+    if (MODE == kPagedTiles) {
+      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + kt / p.page_size];
+      clean = clean && blk >= 0 && blk < p.num_blocks;
+      if (!(blk >= 0 && blk < p.num_blocks)) {
+        const u32x4v z = {0u, 0u, 0u, 0u};
+        t.va0 = z; t.vb0 = z; t.va1 = z; t.vb1 = z;
       }
-      if (key + 1 < sk) {
-        int64_t prow;
-        if (one_page_tiles) prow = tile_ok ? tile_row0 + 2 * kp + 1 : -1;
-        else prow = key_row(p, b, k0, key + 1);
-        if (prow >= 0)
-          vb = *reinterpret_cast<const u32x4v*>(p.v + prow * p.v_row_stride + (int64_t)g * kHeadDim + dc * 8);
-      }
-      uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt_lds);
+    }
+    if (MODE != kPagedRows && !clean) {
+      const u32x4v z = {0u, 0u, 0u, 0u};
+      const int n = sk - kt;
+      if (2 * r0 >= n) t.va0 = z;
+      if (2 * r0 + 1 >= n) t.vb0 = z;
+      if (2 * r0 + 32 >= n) t.va1 = z;
+      if (2 * r0 + 33 >= n) t.vb1 = z;
+    }
+    if (MODE == kPagedRows) {  // rows that resolved to no cache row read row 0: zero them
+      const u32x4v z = {0u, 0u, 0u, 0u};
+      if (paged_row(kt + 2 * r0) < 0) t.va0 = z;
+      if (paged_row(kt + 2 * r0 + 1) < 0) t.vb0 = z;
+      if (paged_row(kt + 2 * r0 + 32) < 0) t.va1 = z;
+      if (paged_row(kt + 2 * r0 + 33) < 0) t.vb1 = z;
+    }
+    *reinterpret_cast<u32x4v*>(k_lds + (r0) * kKS + dc * 8) = t.k0;
+    *reinterpret_cast<u32x4v*>(k_lds + (r0 + 16) * kKS + dc * 8) = t.k1;
+    *reinterpret_cast<u32x4v*>(k_lds + (r0 + 32) * kKS + dc * 8) = t.k2;
+    *reinterpret_cast<u32x4v*>(k_lds + (r0 + 48) * kKS + dc * 8) = t.k3;
+    uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt_lds);
+    auto put = [&](int kp, const u32x4v& va, const u32x4v& vb) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t a = va[e], c = vb[e];
-        // d = dc*8 + 2e holds the low halves, d + 1 the high halves.
+        // d = dc*8 + 2e takes the low halves of both keys, d + 1 the high halves.
         vt32[((dc * 8 + 2 * e) * kVS + 2 * kp) >> 1] = (a & 0xffffu) | (c << 16);
         vt32[((dc * 8 + 2 * e + 1) * kVS + 2 * kp) >> 1] = (a >> 16) | (c & 0xffff0000u);
       }
-    }
+    };
+    put(r0, t.va0, t.vb0);
+    put(r0 + 16, t.va1, t.vb1);
+  };
+
+  TileRegs next;
+  if (k_begin < k_end) next = load_tile(k_begin);
+  for (int kt = k_begin; kt < k_end; kt += kTileK) {
+    __syncthreads();  // every wave is done reading the previous tile
+    store_tile(next, kt);
     __syncthreads();
+    // Prefetch the following tile: its loads are in flight during this tile's math.
+    if (kt + kTileK < k_end) next = load_tile(kt + kTileK);
 
     // ---- S^T = K Q^T for two 32-key blocks ----
     f32x16 s[2];
@@ -204,8 +275,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
     }
 
     // ---- mask: element e = 4i + j of block kb is key kt + 32kb + 8i + 4hf + j ----
-    const bool need_mask = (kt + kTileK - 1 > blk_min_limit) || (kt + kTileK > k_end);
-    if (need_mask) {
+    if ((kt + kTileK - 1 > blk_min_limit) || (kt + kTileK > k_end)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -215,16 +285,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
         }
     }
 
-    // ---- online softmax (per lane = per column; the two half-waves share the max) ----
+    // ---- online softmax (lane = column; the two half-waves share the max) ----
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float m_base = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
-    const float alpha = fast_exp2(m * p.scale_log2 - m_base);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.scale_log2;
+    const bool grow = mx > mb_run + kRescaleThreshold;
+    if (__builtin_amdgcn_ballot_w64(grow)) {  // rare after the first tile
+      const float mb_new = grow ? mx : mb_run;
+      const float alpha = grow ? fast_exp2(mb_run - mb_new) : 1.f;  // first growth: 2^-inf = 0
+      mb_run = mb_new;
+      l *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[mb][e] *= alpha;
+    }
+    const float m_base = (mb_run == -INFINITY) ? 0.f : mb_run;
     float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -234,12 +313,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
         s[kb][e] = pe;
         rs += pe;
       }
-    l = l * alpha + rs;
-    m = m_new;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[mb][e] *= alpha;
+    l += rs;
 
     // ---- P^T as bf16 B operands: chunk c of block kb = elements 8c..8c+7 ----
     bf16x8 pk[2][2];
@@ -299,7 +373,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
       }
     if (hf == 0) {
       float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
-      ml[0] = (m == -INFINITY) ? -INFINITY : m * p.scale_log2;
+      ml[0] = mb_run;
       ml[1] = l_tot;
     }
   }
@@ -307,40 +381,49 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
 
 // Merge the split-KV partials of one query tile:
 //   O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,  M = max_s m_s.
+// grid = (combine items, kCols / kCombineCols): a workgroup owns kCombineCols
+// columns; each lane owns one 4-float slice of one column's output row, so
+// the split loop's loads are independent and overlap.
+constexpr int kCombineCols = kThreads / (kHeadDim / 4);  // 8 columns per workgroup
+
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) {
   const int32_t* it = p.combine + (int64_t)blockIdx.x * kItemInts;
   const int b = it[0], g = it[1], q_start = it[2], q_count = it[3];
   const int first = it[4], nsplit = it[5];
-  const int q0 = p.cu_q[b];
-  for (int u = threadIdx.x; u < kCols * (kHeadDim / 4); u += kThreads) {
-    const int col = u / (kHeadDim / 4);
-    const int d = 4 * (u - col * (kHeadDim / 4));
-    const int pos = col / p.group;
-    if (pos >= q_count) continue;
-    const int hh = col - pos * p.group;
-    float mmax = -INFINITY;
-    for (int s = 0; s < nsplit; ++s)
-      mmax = fmaxf(mmax, p.part_ml[((int64_t)(first + s) * kCols + col) * 2]);
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float lsum = 0.f;
-    if (mmax != -INFINITY) {
-      for (int s = 0; s < nsplit; ++s) {
-        const float* ml = p.part_ml + ((int64_t)(first + s) * kCols + col) * 2;
-        const float w = fast_exp2(ml[0] - mmax);
-        lsum += w * ml[1];
-        const float4 v = *reinterpret_cast<const float4*>(
-            p.part_o + ((int64_t)(first + s) * kCols + col) * kHeadDim + d);
-        acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
-      }
+  const int col = blockIdx.y * kCombineCols + threadIdx.x / (kHeadDim / 4);
+  const int d = 4 * (threadIdx.x % (kHeadDim / 4));
+  const int pos = col / p.group;
+  if (pos >= q_count) return;
+  const int hh = col - pos * p.group;
+  const float* ml = p.part_ml + ((int64_t)first * kCols + col) * 2;
+  const float* po = p.part_o + ((int64_t)first * kCols + col) * kHeadDim + d;
+  const int64_t ml_stride = (int64_t)kCols * 2;
+  const int64_t po_stride = (int64_t)kCols * kHeadDim;
+  float mmax = -INFINITY;
+#pragma unroll 8
+  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, ml[s * ml_stride]);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.f;
+  if (mmax != -INFINITY) {
+#pragma unroll 4
+    for (int s = 0; s < nsplit; ++s) {
+      const float2 mls = *reinterpret_cast<const float2*>(ml + s * ml_stride);
+      const float4 v = *reinterpret_cast<const float4*>(po + s * po_stride);
+      const float w = fast_exp2(mls.x - mmax);
+      lsum += w * mls.y;
+      acc.x += w * v.x;
+      acc.y += w * v.y;
+      acc.z += w * v.z;
+      acc.w += w * v.w;
     }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
-                     (int64_t)(g * p.group + hh) * kHeadDim + d;
-    u32x2v w;
-    w[0] = pack_bf16x2(acc.x * inv, acc.y * inv);
-    w[1] = pack_bf16x2(acc.z * inv, acc.w * inv);
-    *reinterpret_cast<u32x2v*>(orow) = w;
   }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  uint16_t* orow = p.out + (int64_t)(p.cu_q[b] + q_start + pos) * p.out_row_stride +
+                   (int64_t)(g * p.group + hh) * kHeadDim + d;
+  u32x2v w;
+  w[0] = pack_bf16x2(acc.x * inv, acc.y * inv);
+  w[1] = pack_bf16x2(acc.z * inv, acc.w * inv);
+  *reinterpret_cast<u32x2v*>(orow) = w;
 }
 
 }  // namespace
@@ -409,11 +492,18 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   prm.scale_log2 = softmax_scale * 1.4426950408889634f;
 
   hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  const int mode = !block_table ? kContiguous : (page_size % kTileK == 0 ? kPagedTiles : kPagedRows);
+  if (mode == kContiguous)
+    hipLaunchKernelGGL(attn_fwd_kernel<kContiguous>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  else if (mode == kPagedTiles)
+    hipLaunchKernelGGL(attn_fwd_kernel<kPagedTiles>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<kPagedRows>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
   int st = launch_status();
   if (st != VLC_OK) return st;
   if (n_comb > 0) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)n_comb), dim3(kThreads), 0, s, prm);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)n_comb, kCols / kCombineCols), dim3(kThreads), 0,
+                       s, prm);
     st = launch_status();
   }
   return st;

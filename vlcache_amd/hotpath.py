@@ -1,0 +1,137 @@
+"""Device state of the warm partial-recompute prefill hot path on synthetic inputs.
+
+One warm request (or a batch of them) runs, per step:
+  1. the all-layer reuse copy of the cached image KV with K re-rotated to the
+     image's new position (one launch; ModelRunner.copy_image_kv,
+     engine/model_runner.py:170-180);
+  2. per layer, the scatter of the recomputed tokens' K/V into the paged cache
+     (store_kvcache, layers/attention.py:62-63) and the varlen paged GQA causal
+     attention of the recomputed queries against the whole cache
+     (layers/attention.py:64-70).
+Inputs are seeded N(0, 1) bf16: cached K/V, the recomputed tokens' q/k/v.
+Block ids are a seeded permutation of the pool; the cached image's blocks and
+each request's blocks are disjoint, as the reference's allocator guarantees
+(the cached entry's blocks stay referenced, engine/block_manager.py:91-94).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import kernels
+from .workloads import BLOCK_SIZE, Workload
+
+
+def _slots(bt, positions):
+    bt = np.asarray(bt, dtype=np.int64)
+    p = np.asarray(positions, dtype=np.int64)
+    return bt[p // BLOCK_SIZE] * BLOCK_SIZE + p % BLOCK_SIZE
+
+
+class WarmPrefillHotPath:
+    def __init__(self, wl: Workload, device, seed: int = 0, rotate: bool = True):
+        self.wl = wl
+        m = wl.model
+        self.model = m
+        self.device = torch.device(device)
+        dev = self.device
+        rng = np.random.default_rng(seed)
+        reqs = wl.requests
+        img_len = reqs[0].n_image
+        cached_prefix = reqs[0].cached_prefix
+        # block pool: one cached-image entry (shared) + each request's own blocks
+        entry_len = cached_prefix + img_len
+        entry_nb = -(-entry_len // BLOCK_SIZE)
+        seq_nbs = [-(-r.length // BLOCK_SIZE) for r in reqs]
+        nb = entry_nb + sum(seq_nbs)
+        perm = rng.permutation(nb)
+        entry_bt = perm[:entry_nb]
+        seq_bts = []
+        p = entry_nb
+        for n in seq_nbs:
+            seq_bts.append(perm[p:p + n])
+            p += n
+        self.num_blocks = nb
+
+        L, hkv, hd, hq = m.num_layers, m.num_kv_heads, m.head_dim, m.num_heads
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.kv_cache = torch.randn(2, L, nb, BLOCK_SIZE, hkv, hd, generator=g, device=dev,
+                                    dtype=torch.bfloat16)
+        self.k_caches = [self.kv_cache[0, l] for l in range(L)]
+        self.v_caches = [self.kv_cache[1, l] for l in range(L)]
+
+        # reuse copy: old -> new slots per request, one rotation segment per request
+        old, new, seg, deltas = [], [], [], []
+        slot_map, bts, cu_q, cu_k = [], [], [0], [0]
+        for i, (r, bt) in enumerate(zip(reqs, seq_bts)):
+            img_s, img_e = r.prefix, r.prefix + r.n_image
+            reuse = np.arange(img_s + r.R, img_e) if r.ratio > 0 else np.arange(0)
+            old.append(_slots(entry_bt, cached_prefix + (reuse - img_s)))
+            new.append(_slots(bt, reuse))
+            seg.append(np.full(reuse.size, i, dtype=np.int32))
+            deltas.append([r.delta] * 3)
+            if r.ratio > 0:
+                comp = np.concatenate([np.arange(0, img_s + r.R), np.arange(img_e, r.length)])
+            else:
+                comp = np.arange(r.length)
+            slot_map.append(_slots(bt, comp))
+            row = np.full(max(seq_nbs), -1, dtype=np.int32)
+            row[:len(bt)] = bt
+            for sq, sk in r.subseqs():
+                cu_q.append(cu_q[-1] + sq)
+                cu_k.append(cu_k[-1] + sk)
+                bts.append(row)
+        self.old_slots = torch.from_numpy(np.concatenate(old)).to(dev)
+        self.new_slots = torch.from_numpy(np.concatenate(new)).to(dev)
+        self.seg = torch.from_numpy(np.concatenate(seg)).to(dev)
+        self.cos_sin = kernels.rerotation_table(deltas, hd, m.rope_theta, m.mrope_section, device=dev)
+        self.rotate = rotate
+        self.n_reused = int(self.old_slots.numel())
+
+        n_q = cu_q[-1]
+        self.n_computed = n_q
+        self.cu_q_host, self.cu_k_host = cu_q, cu_k
+        self.cu_q = torch.tensor(cu_q, dtype=torch.int32, device=dev)
+        self.cu_k = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+        self.slot_mapping = torch.from_numpy(np.concatenate(slot_map).astype(np.int32)).to(dev)
+        self.block_tables = torch.from_numpy(np.stack(bts)).to(dev)
+        # recomputed tokens: qkv rows as the QKV projection lays them out; k is a
+        # separate contiguous tensor (it comes out of RoPE), v a strided view
+        qkv = torch.randn(n_q, (hq + 2 * hkv) * hd, generator=g, device=dev, dtype=torch.bfloat16)
+        self.q = qkv[:, :hq * hd].reshape(n_q, hq, hd).contiguous()
+        self.k = qkv[:, hq * hd:(hq + hkv) * hd].reshape(n_q, hkv, hd).contiguous()
+        self.v = qkv[:, (hq + hkv) * hd:].view(n_q, hkv, hd)
+        self.qkv = qkv
+        self.scale = hd ** -0.5
+        # Block tables exist only when a request is partial; otherwise attention
+        # reads the fresh contiguous k/v (engine/model_runner.py:294-299,
+        # layers/attention.py:65-66).
+        self.paged = any(r.ratio > 0 for r in reqs)
+        self.plan = kernels.plan_attention(cu_q, cu_k, hq, hkv, hd, True, dev)
+        self.out = torch.empty(n_q, hq, hd, dtype=torch.bfloat16, device=dev)
+
+    # ---- the three kernels ----
+    def rerotate(self):
+        kernels.rerotate_copy_kv(self.kv_cache, self.old_slots, self.new_slots, self.cos_sin, self.seg,
+                                 rotate_k=self.rotate)
+
+    def scatter(self, layer: int):
+        kernels.store_kvcache_raw(self.k, self.v, self.k_caches[layer], self.v_caches[layer],
+                                  self.slot_mapping)
+
+    def attention(self, layer: int):
+        if not self.paged:
+            return kernels.varlen_attention(self.q, self.k, self.v, self.cu_q, self.cu_k, self.scale, True,
+                                            None, plan=self.plan, out=self.out)
+        return kernels.varlen_attention(self.q, self.k_caches[layer], self.v_caches[layer], self.cu_q,
+                                        self.cu_k, self.scale, True, self.block_tables, plan=self.plan,
+                                        out=self.out)
+
+    def step(self):
+        if self.n_reused:
+            self.rerotate()
+        for layer in range(self.model.num_layers):
+            self.scatter(layer)
+            self.attention(layer)
+        return self.out
