@@ -1,0 +1,159 @@
+"""CPU tests of the C-ABI library: it loads, exports every declared symbol, and
+the host-side attention planner produces a work list that covers the problem.
+
+No kernel is launched here (no GPU in this environment).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from vlcache_amd import _lib, kernels, workloads
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from vlcache_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "vlc_capi.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vlc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared_symbols()
+    assert {"vlc_store_kvcache", "vlc_rerotate_copy_kv", "vlc_attn_plan", "vlc_varlen_attn_fwd"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_status_strings(lib):
+    assert lib.vlc_abi_version() == _lib.ABI_VERSION
+    assert lib.vlc_status_string(0) == b"ok"
+    assert b"unsupported" in lib.vlc_status_string(-2)
+
+
+def _items(plan):
+    h = plan.host
+    n_items, n_comb = int(h[1]), int(h[2])
+    items = h[16:16 + 8 * n_items].reshape(-1, 8)
+    comb = h[16 + 8 * n_items:16 + 8 * (n_items + n_comb)].reshape(-1, 8)
+    return items, comb
+
+
+def _check_plan_covers(cu_q, cu_k, hq, hkv, causal, num_cus):
+    plan = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, causal, "cpu", num_cus=num_cus)
+    items, comb = _items(plan)
+    group = hq // hkv
+    ppt = 128 // group
+    assert int(plan.host[5]) == ppt
+    # every (seq, kv head, query tile) is covered; split ranges partition [0, kmax) in 64-key steps
+    expect = {}
+    for b in range(len(cu_q) - 1):
+        sq, sk = cu_q[b + 1] - cu_q[b], cu_k[b + 1] - cu_k[b]
+        for qs in range(0, sq, ppt):
+            qc = min(ppt, sq - qs)
+            kmax = max(0, min(sk, qs + qc + sk - sq)) if causal else sk
+            for g in range(hkv):
+                expect[(b, g, qs)] = (qc, kmax)
+    got = {}
+    slots_seen = []
+    for it in items:
+        b, g, qs, qc, kb, ke, slot = (int(x) for x in it[:7])
+        assert expect[(b, g, qs)][0] == qc
+        got.setdefault((b, g, qs), []).append((kb, ke, slot))
+        assert kb % 64 == 0 and kb <= ke
+        if slot >= 0:
+            slots_seen.append(slot)
+    assert set(got) == set(expect)
+    comb_of = {(int(c[0]), int(c[1]), int(c[2])): (int(c[4]), int(c[5])) for c in comb}
+    for key, ranges in got.items():
+        kmax = expect[key][1]
+        ranges.sort()
+        if len(ranges) == 1:
+            assert ranges[0] == (0, kmax, -1)
+            assert key not in comb_of
+        else:
+            first, n = comb_of[key]
+            assert n == len(ranges)
+            assert [r[2] for r in ranges] == list(range(first, first + n))
+            assert ranges[0][0] == 0 and ranges[-1][1] == kmax
+            for a, c in zip(ranges, ranges[1:]):
+                assert a[1] == c[0]
+    assert sorted(slots_seen) == list(range(int(plan.host[3])))
+    # longest-first order
+    cost = [max(1, -(-(int(i[5]) - int(i[4])) // 64)) for i in items]
+    assert cost == sorted(cost, reverse=True)
+    return plan
+
+
+@pytest.mark.parametrize("num_cus", [1, 8, 256, 4096])
+def test_plan_covers_warm_request(lib, num_cus):
+    _check_plan_covers([0, 1183, 1247], [0, 1183, 11924], 16, 2, True, num_cus)
+
+
+def test_plan_covers_ragged_and_group7(lib):
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        n = int(rng.integers(1, 6))
+        sq = rng.integers(0, 400, n)
+        sk = sq + rng.integers(-20, 3000, n)
+        sk = np.maximum(sk, 0)
+        cu_q = [0] + list(np.cumsum(sq).astype(int))
+        cu_k = [0] + list(np.cumsum(sk).astype(int))
+        hq, hkv = [(16, 2), (28, 4), (8, 8), (32, 2)][int(rng.integers(0, 4))]
+        _check_plan_covers(cu_q, cu_k, hq, hkv, bool(rng.integers(0, 2)), int(rng.integers(1, 512)))
+
+
+def test_plan_rejects_bad_shapes(lib):
+    with pytest.raises(_lib.VLCError) as e:
+        kernels.plan_attention([0, 4], [0, 4], 16, 2, 64, True, "cpu")
+    assert e.value.status == -2
+    with pytest.raises(_lib.VLCError) as e:
+        kernels.plan_attention([0, 4], [0, 4], 15, 2, 128, True, "cpu")
+    assert e.value.status == -1
+    # capacity protocol: a too-small buffer reports the needed length
+    cu = np.array([0, 300], dtype=np.int32)
+    n = ctypes.c_int64(0)
+    ws = ctypes.c_int64(0)
+    ip = ctypes.POINTER(ctypes.c_int32)
+    buf = np.zeros(4, dtype=np.int32)
+    st = lib.vlc_attn_plan(cu.ctypes.data_as(ip), cu.ctypes.data_as(ip), 1, 16, 2, 128, 1, 256,
+                           buf.ctypes.data_as(ip), buf.size, ctypes.byref(n), ctypes.byref(ws))
+    assert st == _lib.VLC_ERR_CAPACITY and n.value > 4
+
+
+def test_kernel_wrappers_refuse_cpu_tensors(lib):
+    q = torch.zeros(4, 16, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 256, 2, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 4], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        kernels.varlen_attention(q, k, k, cu, cu, 0.1, True, torch.zeros(1, 1, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        kernels.store_kvcache_raw(torch.zeros(4, 2, 128), torch.zeros(4, 2, 128), k, k,
+                                  torch.zeros(4, dtype=torch.int32))
+
+
+def test_workload_counts_match_hand_derivation():
+    # unmasked (query, key) pairs x 4 * hd * Hq: cfg1 49,372 pairs; cfg2 1,385,744; cfg3 57,689,911
+    for wl, pairs in ((workloads.cfg1(), 49372), (workloads.cfg2(), 1385744), (workloads.cfg3(), 57689911)):
+        cu_q, cu_k = wl.cu_seqlens()
+        assert workloads.attention_flops(cu_q, cu_k, 16, 128) == 4 * 128 * 16 * pairs
+    assert workloads.merged_grid(3840, 2160) == (77, 137)
+    assert workloads.merged_grid(1920, 1080) == (39, 69)
+    r = workloads.cfg2().requests[0]
+    assert (r.R, r.n_reused, r.n_computed, r.delta) == (1055, 9494, 1247, 88)
