@@ -1,0 +1,206 @@
+"""GPU tests of the drop-in surface: Attention/store_kvcache through the Context,
+ModelRunner.copy_image_kv, and the warm request through LLM end to end.
+
+End-to-end checks use a small random-init model with Qwen2.5-VL attention
+shapes (head_dim 128, GQA 2:1, M-RoPE sections [16, 24, 24]):
+  * a warm request whose text prefix and image equal the cached request's
+    reuses exactly the KV a full recompute produces, so its first-token logits
+    match the full recompute's;
+  * with a shifted prefix, the reused layer-0 keys re-rotated to the new
+    positions match layer-0 keys computed fresh at those positions (layer 0's
+    K depends only on the token and its position).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oattn
+from oracle import rope as orope
+from oracle import scatter as oscat
+from tests._util import assert_close, bits, gen, randn_bf16, say
+from vlcache_amd import SamplingParams
+from vlcache_amd.layers.attention import Attention
+from vlcache_amd.utils.context import reset_context, set_context
+
+pytestmark = pytest.mark.gpu
+
+IMG = 999
+TINY = dict(hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+            num_key_value_heads=2, vocab_size=1000, rms_norm_eps=1e-6, rope_theta=1e6,
+            rope_scaling={"type": "mrope", "mrope_section": [16, 24, 24]}, max_position_embeddings=4096,
+            tie_word_embeddings=True, image_token_id=IMG, spatial_merge_size=2, eos_token_id=0,
+            torch_dtype="bfloat16")
+
+
+def test_attention_layer_paged_prefill_through_context(dev):
+    say("layer: Attention.forward, paged prefill (2 sub-sequences), plan built from the context")
+    hq, hkv, page = 16, 2, 256
+    g = gen(40)
+    nb = 8
+    kc = torch.randn(nb, page, hkv, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, page, hkv, 128, generator=g).to(torch.bfloat16)
+    bt = torch.tensor([[5, 2, 7, -1], [5, 2, 7, -1]], dtype=torch.int32)
+    cu_q, cu_k = [0, 300, 340], [0, 300, 700]
+    q = randn_bf16((340, hq, 128), 41)
+    k_new = randn_bf16((340, hkv, 128), 42)
+    qkv_v = randn_bf16((340, 2560), 43)
+    slots = np.concatenate([np.arange(300), np.arange(660, 700)])
+    slot_phys = torch.tensor([bt[0, s // page].item() * page + s % page for s in slots], dtype=torch.int32)
+    attn = Attention(hq, 128, 128 ** -0.5, hkv)
+    attn.k_cache, attn.v_cache = kc.to(dev), vc.to(dev)
+    v_dev = qkv_v.to(dev)[:, 2304:].view(340, hkv, 128)
+    set_context(True, torch.tensor(cu_q, dtype=torch.int32, device=dev), torch.tensor(cu_k, dtype=torch.int32,
+                device=dev), 300, 700, slot_phys.to(dev), None, bt.to(dev))
+    out = attn(q.to(dev), k_new.to(dev), v_dev).cpu()
+    reset_context()
+    kref, vref = kc.clone(), vc.clone()
+    oscat.store_kvcache(k_new.view(torch.int16).numpy(), qkv_v[:, 2304:].reshape(340, hkv, 128).contiguous()
+                        .view(torch.int16).numpy(), kref.view(torch.int16).numpy(), vref.view(torch.int16).numpy(),
+                        slot_phys.numpy())
+    assert np.array_equal(bits(attn.k_cache), bits(kref)) and np.array_equal(bits(attn.v_cache), bits(vref))
+    ref = oattn.varlen_attention(q, kref, vref, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), page)
+    assert_close(out, ref, what="Attention paged prefill")
+
+
+def test_attention_layer_decode(dev):
+    say("layer: Attention.forward decode, 3 sequences, [B, 1, Hq, hd] output")
+    hq, hkv, page = 16, 2, 256
+    kc = randn_bf16((6, page, hkv, 128), 44)
+    vc = randn_bf16((6, page, hkv, 128), 45)
+    lens = [10, 300, 257]
+    bt = torch.tensor([[0, -1], [1, 2], [3, 4]], dtype=torch.int32)
+    q = randn_bf16((3, hq, 128), 46)
+    k1 = randn_bf16((3, hkv, 128), 47)
+    v1 = randn_bf16((3, hkv, 128), 48)
+    slot = torch.tensor([bt[i, (n - 1) // page].item() * page + (n - 1) % page for i, n in enumerate(lens)],
+                        dtype=torch.int32)
+    attn = Attention(hq, 128, 128 ** -0.5, hkv)
+    attn.k_cache, attn.v_cache = kc.to(dev), vc.to(dev)
+    cu_q, cu_k = [0, 1, 2, 3], [0, 10, 310, 567]
+    set_context(False, torch.tensor(cu_q, dtype=torch.int32, device=dev), torch.tensor(cu_k, dtype=torch.int32,
+                device=dev), 1, 300, slot.to(dev), torch.tensor(lens, dtype=torch.int32, device=dev), bt.to(dev),
+                cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
+    out = attn(q.to(dev), k1.to(dev), v1.to(dev)).cpu()
+    reset_context()
+    assert out.shape == (3, 1, hq, 128)
+    kref, vref = kc.clone(), vc.clone()
+    kref.view(-1, hkv, 128)[slot.long()] = k1
+    vref.view(-1, hkv, 128)[slot.long()] = v1
+    ref = oattn.varlen_attention(q, kref, vref, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), page)
+    assert_close(out[:, 0], ref, what="Attention decode")
+
+
+def _engine(ratio, blocks=64, seed=0):
+    from vlcache_amd import LLM
+
+    return LLM(dict(TINY), recompute_ratio=ratio, num_kvcache_blocks=blocks, max_model_len=4096, seed=seed,
+               enforce_eager=True)
+
+
+def _request(prefix, grid, suffix, seed):
+    t, h, w = grid
+    n_img = t * (h // 2) * (w // 2)
+    rng = np.random.default_rng(seed)
+    toks = ([int(x) for x in rng.integers(1, 900, prefix)] + [IMG] * n_img
+            + [int(x) for x in rng.integers(1, 900, suffix)])
+    pv = torch.linspace(0, 1, t * h * w)[:, None]  # stands in for pixel patches; only hashed
+    return toks, {"pixel_values": pv, "image_grid_thw": torch.tensor([list(grid)])}
+
+
+def _prefill_logits(engine, toks, mm):
+    """Schedule one prompt, run the reuse copy if partial, return (seq, first-token logits)."""
+    from vlcache_amd.utils.context import reset_context as rc
+
+    seq = engine.add_request(toks, SamplingParams(temperature=1.0, max_tokens=1), mm)
+    seqs, is_prefill = engine.scheduler.schedule()
+    assert is_prefill and seqs == [seq]
+    engine._do_image_kv_copy(seqs)
+    runner = engine.model_runner
+    with torch.inference_mode():
+        ids, pos, mmi = runner.prepare_prefill(seqs)
+        logits, _ = runner.run_model(ids, pos, True, mmi)
+        if runner._logit_indices is not None:
+            logits = logits[runner._logit_indices]
+    rc()
+    engine._store_image_kv(seqs)
+    torch.cuda.synchronize()
+    return seq, logits.float().cpu()
+
+
+def test_warm_request_equals_full_recompute_for_same_prefix(dev):
+    say("engine: warm partial request (same prefix + image) vs full recompute, first-token logits")
+    grid = (1, 20, 24)  # 120 image tokens
+    toks_a, mm = _request(40, grid, 12, seed=1)
+    toks_b = toks_a[:40 + 120] + [int(x) for x in np.random.default_rng(2).integers(1, 900, 9)]
+    warm = _engine(0.25)
+    _prefill_logits(warm, toks_a, mm)          # cold: caches the image KV
+    seq_b, lw = _prefill_logits(warm, toks_b, mm)
+    assert seq_b.is_partial_recompute and seq_b.num_recompute_tokens == 30
+    full = _engine(0.0)
+    _, lf = _prefill_logits(full, toks_b, mm)
+    assert_close(lw, lf, atol=5e-2, cos_min=0.999, what="warm vs full logits")
+
+
+def _layer0_rows(engine, plane, slots, dev):
+    kv = engine.model_runner.kv_cache[plane, 0].view(-1, 2, 128)
+    return kv[torch.as_tensor(np.asarray(slots), device=dev)].float().cpu()
+
+
+def test_warm_request_rerotates_reused_keys_to_new_positions(dev):
+    say("engine: shifted prefix (24 -> 61 tokens): re-rotated layer-0 K vs fresh layer-0 K")
+    grid = (1, 16, 20)  # 80 image tokens
+    toks_a, mm = _request(24, grid, 7, seed=3)
+    toks_b, _ = _request(61, grid, 5, seed=4)
+    warm = _engine(0.1)
+    seq_a, _ = _prefill_logits(warm, toks_a, mm)
+    R = 8  # ceil(0.1 * 80)
+    q_img = np.arange(R, 80)  # reused image-token offsets
+    pa = 24 + q_img
+    stale = _layer0_rows(warm, 0, np.asarray(seq_a.block_table)[pa // 256] * 256 + pa % 256, dev)
+    seq_b, _ = _prefill_logits(warm, toks_b, mm)
+    assert seq_b.is_partial_recompute and seq_b.num_recompute_tokens == R
+    pb = 61 + q_img
+    kw = _layer0_rows(warm, 0, np.asarray(seq_b.block_table)[pb // 256] * 256 + pb % 256, dev)
+    vw = _layer0_rows(warm, 1, np.asarray(seq_b.block_table)[pb // 256] * 256 + pb % 256, dev)
+    full = _engine(0.0)
+    seq_f, _ = _prefill_logits(full, toks_b, mm)
+    kf = _layer0_rows(full, 0, np.asarray(seq_f.block_table)[pb // 256] * 256 + pb % 256, dev)
+    vf = _layer0_rows(full, 1, np.asarray(seq_f.block_table)[pb // 256] * 256 + pb % 256, dev)
+    assert_close(vw, vf, what="layer-0 V of reused tokens")
+    assert_close(kw, kf, what="layer-0 re-rotated K vs fresh K")
+    # the cached keys at their old positions are far from the fresh ones: the rotation matters
+    assert (kw - kf).abs().max() < 0.5 * (stale - kf).abs().max()
+
+
+def test_model_runner_copy_image_kv_plain_and_rotated(dev):
+    say("runner: copy_image_kv without deltas (bit copy) and with deltas (re-rotation)")
+    eng = _engine(0.1, blocks=8)
+    r = eng.model_runner
+    g = gen(50)
+    r.kv_cache.copy_(torch.randn(r.kv_cache.shape, generator=g).to(torch.bfloat16))
+    before = r.kv_cache.cpu()
+    old = np.arange(100, 400)
+    new = np.arange(1200, 1500)
+    r.copy_image_kv(old, new)
+    ref = before.clone()
+    oscat.copy_image_kv(ref.view(torch.int16).numpy(), old, new)
+    assert np.array_equal(bits(r.kv_cache), bits(ref))
+    r.copy_image_kv(old, new + 300, [[9, 9, 9]])
+    cs = orope.rerotation_cos_sin([[9, 9, 9]], 128, 1e6, [16, 24, 24])
+    orope.rerotate_copy_kv(ref, old, new + 300, cs)
+    assert np.array_equal(bits(r.kv_cache), bits(ref))
+
+
+def test_generate_runs_prefill_and_decode(dev):
+    say("engine: LLM.generate cold + warm with 3 decode steps each")
+    eng = _engine(0.1)
+    toks_a, mm = _request(16, (1, 8, 8), 4, seed=5)
+    toks_b, _ = _request(20, (1, 8, 8), 6, seed=6)
+    sp = SamplingParams(temperature=0.6, max_tokens=3, ignore_eos=True)
+    out = eng.generate([toks_a], sp, mm_inputs=[mm])
+    out += eng.generate([toks_b], sp, mm_inputs=[mm])
+    assert [len(o["token_ids"]) for o in out] == [3, 3]
+    assert all(o["ttft"] > 0 for o in out)
+    assert len(eng.scheduler.block_manager.image_kv_cache) == 1

@@ -1,0 +1,265 @@
+"""Per-GPU executor (engine/model_runner.py of the reference), one GPU.
+
+Same method surface: call, copy_image_kv, prepare_prefill, prepare_decode,
+prepare_sample, run_model, run, allocate_kv_cache, exit.  Differences:
+  * copy_image_kv(old_slots, new_slots, deltas=None, seg_of_token=None) runs the
+    all-layer reuse copy as one gfx950 kernel; with deltas it also re-rotates K
+    to the image's new rotary position (without deltas it is the reference's
+    plain copy, bit for bit);
+  * prepare_prefill builds the step's attention work plan once (host lists are
+    at hand) and passes it through the Context to every layer;
+  * positions are M-RoPE [3, N] when the model config has mrope_section and
+    use_mrope is set, else the reference's 1-D positions;
+  * host preparation is vectorised (numpy) instead of per-token Python loops;
+  * no tensor parallelism, no shared-memory RPC: one process, one GPU.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import kernels
+from ..config import Config
+from ..qwen_vl import Qwen2_5_VLForConditionalGeneration, Sampler, random_init_
+from ..utils.context import get_context, reset_context, set_context
+from .sequence import Sequence
+
+
+def _slots(block_table, positions: np.ndarray, block_size: int) -> np.ndarray:
+    bt = np.asarray(block_table, dtype=np.int64)
+    return bt[positions // block_size] * block_size + positions % block_size
+
+
+def _h2d(arr, dtype, device):
+    t = torch.from_numpy(np.ascontiguousarray(arr)).to(dtype)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
+class ModelRunner:
+
+    def __init__(self, config: Config, rank: int = 0, event=None):
+        assert rank == 0 and config.tensor_parallel_size == 1
+        self.config = config
+        hf = config.hf_config
+        self.block_size = config.kvcache_block_size
+        self.enforce_eager = config.enforce_eager
+        self.world_size = 1
+        self.rank = 0
+        self.device = torch.device("cuda", 0)
+        torch.cuda.set_device(self.device)
+        self.dtype = hf.torch_dtype
+        with torch.device(self.device):
+            self.model = Qwen2_5_VLForConditionalGeneration(hf).to(self.dtype)
+        random_init_(self.model, seed=config.seed)
+        self.model.eval()
+        self.sampler = Sampler()
+        self.encoder_cache: dict[int, torch.Tensor] = {}
+        self.num_layers = hf.num_hidden_layers
+        self.num_kv_heads = hf.num_key_value_heads
+        self.num_heads = hf.num_attention_heads
+        self.head_dim = hf.head_dim
+        self._logit_indices = None
+        self.allocate_kv_cache()
+
+    def call(self, method_name, *args):
+        return getattr(self, method_name)(*args)
+
+    def exit(self):
+        torch.cuda.synchronize()
+
+    # ------------------------------------------------------------------ memory
+    def allocate_kv_cache(self):
+        config = self.config
+        block_bytes = 2 * self.num_layers * self.block_size * self.num_kv_heads * self.head_dim * self.dtype.itemsize
+        if config.num_kvcache_blocks <= 0:
+            free, total = torch.cuda.mem_get_info()
+            budget = free - total * (1.0 - config.gpu_memory_utilization)
+            budget *= 1.0 - config.encoder_cache_ratio
+            config.num_kvcache_blocks = int(budget) // block_bytes
+        assert config.num_kvcache_blocks > 0
+        self.kv_cache = torch.empty(2, self.num_layers, config.num_kvcache_blocks, self.block_size,
+                                    self.num_kv_heads, self.head_dim, dtype=self.dtype, device=self.device)
+        layer_id = 0
+        for module in self.model.modules():
+            if hasattr(module, "k_cache") and hasattr(module, "v_cache"):
+                module.k_cache = self.kv_cache[0, layer_id]
+                module.v_cache = self.kv_cache[1, layer_id]
+                layer_id += 1
+        assert layer_id == self.num_layers
+
+    # ------------------------------------------------------------------ reuse copy
+    @torch.inference_mode()
+    def copy_image_kv(self, old_slots, new_slots, deltas=None, seg_of_token=None):
+        """Copy reused image KV of every layer from old to new slots; re-rotate K by `deltas`.
+
+        deltas: None (plain copy) or [num_segments][3] (dt, dh, dw) rotary shifts;
+        seg_of_token: segment of each token (None = all segment 0).
+        """
+        old = np.asarray(old_slots, dtype=np.int64)
+        if old.size == 0:
+            return
+        old_t = _h2d(old, torch.int64, self.device)
+        new_t = _h2d(np.asarray(new_slots, dtype=np.int64), torch.int64, self.device)
+        rotate = deltas is not None and self.config.rerotate_reused_kv and bool(np.any(np.asarray(deltas)))
+        cos_sin = seg = None
+        if rotate:
+            hf = self.config.hf_config
+            section = (hf.rope_scaling or {}).get("mrope_section") if self.config.use_mrope else None
+            cos_sin = kernels.rerotation_table(deltas, self.head_dim, hf.rope_theta, section, device=self.device)
+            if seg_of_token is not None:
+                seg = _h2d(np.asarray(seg_of_token, dtype=np.int32), torch.int32, self.device)
+        kernels.rerotate_copy_kv(self.kv_cache, old_t, new_t, cos_sin, seg, rotate_k=rotate)
+
+    # ------------------------------------------------------------------ step preparation
+    def _positions(self, seq: Sequence, start: int, end: int) -> np.ndarray:
+        pos = getattr(seq, "rope_positions", None)
+        if pos is None:
+            p = np.arange(start, end, dtype=np.int64)
+            return np.tile(p, (3, 1)) if self.config.use_mrope else p
+        return pos[:, start:end] if self.config.use_mrope else pos[0, start:end]
+
+    def prepare_prefill(self, seqs: list[Sequence]):
+        input_ids, positions, slot_mapping = [], [], []
+        cu_q, cu_k = [0], [0]
+        max_q = max_k = 0
+        vbts = []
+        logit_indices = []
+        vidx = 0
+        has_partial = False
+        mm = {"image_hashes": [], "image_grid_thw": [], "image_embeds": [], "recompute": []}
+        has_mm = False
+        for seq in seqs:
+            n = len(seq)
+            ids = np.asarray(seq.token_ids, dtype=np.int64)
+            if seq.mm_inputs:
+                has_mm = True
+                grids = seq.mm_inputs.get("image_grid_thw")
+                embeds = seq.mm_inputs.get("image_embeds")
+                for i in range(0 if grids is None else grids.shape[0]):
+                    mm["image_hashes"].append(seq.image_hashes[i])
+                    mm["image_grid_thw"].append(tuple(int(x) for x in grids[i]))
+                    mm["image_embeds"].append(None if embeds is None else embeds[i])
+                    mm["recompute"].append(seq.num_recompute_tokens if seq.is_partial_recompute else 0)
+            if seq.is_partial_recompute:
+                has_partial = True
+                a, e = seq.image_token_range
+                R = seq.num_recompute_tokens
+                runs = [(0, a + R), (e, n)]  # (sub1: Q = K = [0, a+R)), (sub2: Q = [e, n), K = [0, n))
+                for qs, qe in runs:
+                    input_ids.append(ids[qs:qe])
+                    positions.append(self._positions(seq, qs, qe))
+                    slot_mapping.append(_slots(seq.block_table, np.arange(qs, qe), self.block_size))
+                    cu_q.append(cu_q[-1] + (qe - qs))
+                    cu_k.append(cu_k[-1] + qe)
+                    max_q, max_k = max(max_q, qe - qs), max(max_k, qe)
+                    vbts.append(seq.block_table)
+                logit_indices.append(vidx + 1)
+                vidx += 2
+            else:
+                input_ids.append(ids)
+                positions.append(self._positions(seq, 0, n))
+                cu_q.append(cu_q[-1] + n)
+                cu_k.append(cu_k[-1] + n)
+                max_q, max_k = max(max_q, n), max(max_k, n)
+                if seq.block_table:
+                    slot_mapping.append(_slots(seq.block_table, np.arange(n), self.block_size))
+                    vbts.append(seq.block_table)
+                logit_indices.append(vidx)
+                vidx += 1
+        block_tables = None
+        if has_partial and vbts:
+            width = max(len(bt) for bt in vbts)
+            bt = np.full((len(vbts), width), -1, dtype=np.int32)
+            for i, row in enumerate(vbts):
+                bt[i, :len(row)] = row
+            block_tables = _h2d(bt, torch.int32, self.device)
+        input_ids = _h2d(np.concatenate(input_ids), torch.int64, self.device)
+        positions = _h2d(np.concatenate(positions, axis=-1), torch.int64, self.device)
+        cu_q_t = _h2d(np.asarray(cu_q), torch.int32, self.device)
+        cu_k_t = _h2d(np.asarray(cu_k), torch.int32, self.device)
+        slots = _h2d(np.concatenate(slot_mapping) if slot_mapping else np.zeros(0), torch.int32, self.device)
+        plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
+                                      self.device)
+        set_context(True, cu_q_t, cu_k_t, max_q, max_k, slots, None, block_tables, attn_plan=plan,
+                    cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
+        self._logit_indices = logit_indices if has_partial else None
+        return input_ids, positions, (mm if has_mm else None)
+
+    def prepare_decode(self, seqs: list[Sequence]):
+        n = len(seqs)
+        input_ids = np.array([s.last_token for s in seqs], dtype=np.int64)
+        lens = np.array([len(s) for s in seqs], dtype=np.int64)
+        pos = lens - 1
+        if self.config.use_mrope:
+            pos = np.tile(pos + np.array([s.rope_delta for s in seqs], dtype=np.int64), (3, 1))
+        slot = np.array([s.block_table[-1] * self.block_size + s.last_block_num_tokens - 1 for s in seqs],
+                        dtype=np.int64)
+        width = max(len(s.block_table) for s in seqs)
+        bt = np.full((n, width), -1, dtype=np.int32)
+        for i, s in enumerate(seqs):
+            bt[i, :len(s.block_table)] = s.block_table
+        cu_q = list(range(n + 1))
+        cu_k = [0] + np.cumsum(lens).tolist()
+        plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
+                                      self.device)
+        set_context(False, _h2d(np.asarray(cu_q), torch.int32, self.device),
+                    _h2d(np.asarray(cu_k), torch.int32, self.device), 1, int(lens.max()),
+                    _h2d(slot, torch.int32, self.device), _h2d(lens, torch.int32, self.device),
+                    _h2d(bt, torch.int32, self.device), attn_plan=plan, cu_seqlens_q_host=cu_q,
+                    cu_seqlens_k_host=cu_k)
+        return _h2d(input_ids, torch.int64, self.device), _h2d(pos, torch.int64, self.device)
+
+    def prepare_sample(self, seqs: list[Sequence]):
+        return _h2d(np.array([s.temperature for s in seqs], dtype=np.float32), torch.float32, self.device)
+
+    # ------------------------------------------------------------------ vision inputs
+    def _image_embeds(self, h: int, grid, given):
+        """Visual embeddings of one image: encoder-cache hit, caller-supplied, or synthetic.
+
+        The vision tower is not part of this path.  On a miss the caller's
+        `image_embeds` are used, else seeded synthetic embeddings stand in for its
+        output; either way they are written to the encoder cache.
+        """
+        if h in self.encoder_cache:
+            return self.encoder_cache[h], 0.0
+        m = self.config.hf_config.spatial_merge_size
+        n = int(grid[0]) * (int(grid[1]) // m) * (int(grid[2]) // m)
+        if given is not None:
+            emb = given.to(self.device, self.dtype)
+        else:
+            g = torch.Generator(device=self.device)
+            g.manual_seed(h & ((1 << 63) - 1))
+            emb = torch.randn(n, self.config.hf_config.hidden_size, generator=g, device=self.device,
+                              dtype=self.dtype)
+        assert emb.shape[0] == n
+        self.encoder_cache[h] = emb
+        return emb, 0.0
+
+    def _process_visual(self, mm: dict):
+        parts = []
+        for h, grid, given, r in zip(mm["image_hashes"], mm["image_grid_thw"], mm["image_embeds"], mm["recompute"]):
+            emb, _ = self._image_embeds(h, grid, given)
+            parts.append(emb[:r] if r > 0 else emb)  # partial: first R embeddings (model_runner.py:398-403)
+        return torch.cat(parts, dim=0) if parts else None
+
+    # ------------------------------------------------------------------ execution
+    @torch.inference_mode()
+    def run_model(self, input_ids, positions, is_prefill, mm=None):
+        visual = self._process_visual(mm) if (is_prefill and mm) else None
+        hidden = self.model(input_ids, positions, visual)
+        return self.model.compute_logits(hidden), 0.0
+
+    @torch.inference_mode()
+    def run(self, seqs: list[Sequence], is_prefill: bool):
+        if is_prefill:
+            input_ids, positions, mm = self.prepare_prefill(seqs)
+        else:
+            input_ids, positions = self.prepare_decode(seqs)
+            mm = None
+        temperatures = self.prepare_sample(seqs)
+        logits, vit_time = self.run_model(input_ids, positions, is_prefill, mm)
+        if is_prefill and self._logit_indices is not None:
+            logits = logits[self._logit_indices]
+        token_ids = self.sampler(logits, temperatures).tolist()
+        reset_context()
+        return token_ids, vit_time

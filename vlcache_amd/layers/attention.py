@@ -1,0 +1,70 @@
+"""Drop-in attention layer and KV scatter for the warm partial-recompute prefill.
+
+Same public surface as layers/attention.py of the reference:
+  * store_kvcache(key, value, k_cache, v_cache, slot_mapping) -- same arguments
+    and preconditions (:33-40); the copy runs in the gfx950 scatter kernel.
+  * Attention(num_heads, head_dim, scale, num_kv_heads) with k_cache/v_cache
+    attributes bound by the model runner and forward(q, k, v) reading the global
+    Context (:43-75): prefill attends through the block table when the step has
+    one (the cache is read back after the scatter, :65-66) and over the fresh
+    contiguous k/v otherwise; decode attends through the block table with one
+    query per sequence and returns [B, 1, Hq, hd] (:71-74).
+Both attention forms run in the gfx950 varlen GQA kernel.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import kernels
+from ..utils.context import Context, get_context
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor) -> None:
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    kernels.store_kvcache_raw(key, value, k_cache, v_cache, slot_mapping)
+
+
+def _plan(context: Context, num_heads: int, num_kv_heads: int, head_dim: int, device):
+    """The step's attention plan; built here (one device-to-host copy) if the caller gave none."""
+    plan = context.attn_plan
+    if plan is None or plan.num_heads_q != num_heads or plan.num_heads_kv != num_kv_heads:
+        cu_q = context.cu_seqlens_q_host or context.cu_seqlens_q.tolist()
+        cu_k = context.cu_seqlens_k_host or context.cu_seqlens_k.tolist()
+        plan = kernels.plan_attention(cu_q, cu_k, num_heads, num_kv_heads, head_dim, True, device)
+        context.attn_plan = plan
+    return plan
+
+
+class Attention(nn.Module):
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() and v_cache.numel():
+            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+        if context.is_prefill:
+            if context.block_tables is not None:
+                k, v = k_cache, v_cache
+            plan = _plan(context, self.num_heads, self.num_kv_heads, self.head_dim, q.device)
+            return kernels.varlen_attention(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k, self.scale,
+                                            True, context.block_tables, plan=plan)
+        # decode: one query per sequence against its cached context
+        plan = _plan(context, self.num_heads, self.num_kv_heads, self.head_dim, q.device)
+        o = kernels.varlen_attention(q, k_cache, v_cache, context.cu_seqlens_q, context.cu_seqlens_k, self.scale,
+                                     True, context.block_tables, plan=plan)
+        return o.unsqueeze(1)

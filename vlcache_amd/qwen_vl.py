@@ -1,0 +1,165 @@
+"""Qwen2.5-VL text decoder: the caller of the attention layer on the hot path.
+
+Mirrors the forward of models/qwen3.py (Qwen3Attention :71-87, decoder layer
+:145-158, model :172-186; with attention_bias absent the reference builds the
+Qwen2.5-VL variant: QKV bias, no q/k norm) and of
+Qwen2_5_VLForConditionalGeneration.forward (models/qwen2_5_vl.py:562-580: the
+image-token rows of the embeddings are replaced by visual embeddings).
+
+GEMMs, norms and the MLP stay on torch (hipBLASLt) and run eagerly; the
+attention of every layer is the gfx950 kernel via layers.attention.Attention.
+The vision tower is not part of this path: visual embeddings come from the
+encoder cache (warm request) or are supplied by the caller.
+Weights are random N(0, 0.02) unless loaded by the caller.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .layers.attention import Attention
+from .layers.rotary_embedding import get_rope
+from .utils.context import get_context
+
+IMAGE_TOKEN_ID = 151655
+
+
+class RMSNorm(nn.Module):
+    """(add +) RMSNorm with fp32 statistics (layers/layernorm.py:16-40)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+
+    def forward(self, x, residual=None):
+        dtype = x.dtype
+        xf = x.float()
+        if residual is not None:
+            xf = xf + residual.float()
+            residual = xf.to(dtype)
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        out = xf.to(dtype) * self.weight
+        return out if residual is None else (out, residual)
+
+
+class DecoderAttention(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.num_heads = cfg.num_attention_heads
+        self.num_kv_heads = cfg.num_key_value_heads
+        self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.qkv_proj = nn.Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=True)
+        self.o_proj = nn.Linear(self.q_size, cfg.hidden_size, bias=False)
+        self.rotary_emb = get_rope(self.head_dim, self.head_dim, cfg.max_position_embeddings,
+                                   getattr(cfg, "rope_theta", 1e6), getattr(cfg, "rope_scaling", None))
+        self.attn = Attention(self.num_heads, self.head_dim, self.head_dim ** -0.5, self.num_kv_heads)
+
+    def forward(self, positions, hidden_states):
+        qkv = self.qkv_proj(hidden_states)
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q = q.view(-1, self.num_heads, self.head_dim)
+        k = k.view(-1, self.num_kv_heads, self.head_dim)
+        v = v.view(-1, self.num_kv_heads, self.head_dim)  # strided view into qkv rows
+        q, k = self.rotary_emb(positions, q, k)
+        o = self.attn(q, k, v)
+        return self.o_proj(o.flatten(1, -1))
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.inter = cfg.intermediate_size
+        self.gate_up_proj = nn.Linear(cfg.hidden_size, 2 * cfg.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+
+    def forward(self, x):
+        gu = self.gate_up_proj(x)
+        return self.down_proj(F.silu(gu[..., :self.inter]) * gu[..., self.inter:])
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.self_attn = DecoderAttention(cfg)
+        self.mlp = MLP(cfg)
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+
+    def forward(self, positions, hidden_states, residual):
+        if residual is None:
+            hidden_states, residual = self.input_layernorm(hidden_states), hidden_states
+        else:
+            hidden_states, residual = self.input_layernorm(hidden_states, residual)
+        hidden_states = self.self_attn(positions, hidden_states)
+        hidden_states, residual = self.post_attention_layernorm(hidden_states, residual)
+        return self.mlp(hidden_states), residual
+
+
+class TextModel(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.layers = nn.ModuleList([DecoderLayer(cfg) for _ in range(cfg.num_hidden_layers)])
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+
+    def forward(self, input_ids, positions, inputs_embeds=None):
+        hidden_states = self.embed_tokens(input_ids) if inputs_embeds is None else inputs_embeds
+        residual = None
+        for layer in self.layers:
+            hidden_states, residual = layer(positions, hidden_states, residual)
+        hidden_states, _ = self.norm(hidden_states, residual)
+        return hidden_states
+
+
+class Qwen2_5_VLForConditionalGeneration(nn.Module):
+    """Text side of Qwen2.5-VL with visual-embedding injection; logits of the last row per sub-sequence."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        self.config = cfg
+        self.model = TextModel(cfg)
+        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+        if getattr(cfg, "tie_word_embeddings", False):
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def forward(self, input_ids, positions, visual_embeds=None):
+        inputs_embeds = self.model.embed_tokens(input_ids)
+        if visual_embeds is not None:
+            mask = input_ids == getattr(self.config, "image_token_id", IMAGE_TOKEN_ID)
+            # The reference asserts the count here (a device-to-host sync); a
+            # mismatch raises inside the masked assignment instead.
+            inputs_embeds[mask] = visual_embeds.to(inputs_embeds.dtype)
+        return self.model(input_ids, positions, inputs_embeds=inputs_embeds)
+
+    def compute_logits(self, hidden_states):
+        ctx = get_context()
+        if ctx.is_prefill:  # last row of every (virtual) sequence (layers/embed_head.py:56-60)
+            hidden_states = hidden_states[ctx.cu_seqlens_q[1:] - 1].contiguous()
+        return self.lm_head(hidden_states)
+
+
+@torch.no_grad()
+def random_init_(model: nn.Module, std: float = 0.02, seed: int = 0) -> None:
+    """N(0, std) weights, zero biases, unit norm weights (synthetic checkpoint)."""
+    g = torch.Generator(device=next(model.parameters()).device)
+    g.manual_seed(seed)
+    for name, p in model.named_parameters():
+        if name.endswith("layernorm.weight") or name.endswith("norm.weight"):
+            p.fill_(1.0)
+        elif name.endswith(".bias"):
+            p.zero_()
+        else:
+            p.normal_(0.0, std, generator=g)
+
+
+class Sampler(nn.Module):
+    """Gumbel-max sampling at temperature (layers/sampler.py:10-15)."""
+
+    def forward(self, logits, temperatures):
+        logits = logits.float().div_(temperatures.unsqueeze(dim=1))
+        probs = torch.softmax(logits, dim=-1)
+        return probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
