@@ -48,6 +48,21 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def _profiled_attention_traffic(wl_name: str):
+    """HBM bytes per attention call (fwd + combine) from the committed rocprofv3 PMC summary."""
+    if wl_name != "cfg2":
+        return None
+    path = os.path.join(ROOT, "profiles", "warm_prefill_3b_4k_r0.1_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("attention_traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def _events(n):
     return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
 
@@ -128,6 +143,45 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
     )
 
 
+def run_ttft(ratio: float, reps: int = 2):
+    """Warm TTFT (ms) of the cold -> warm protocol of the reference's test_partial_recompute.py.
+
+    Random-init Qwen2.5-VL-3B (36 layers); each image is the 4K grid (1, 154, 274)
+    -> 10549 tokens.  Per repetition, a fresh image is sent cold (text prefix 40,
+    suffix 64) and then warm (prefix 128, suffix 64).  TTFT is the engine's own
+    clock: from request creation to the sampled first token on the host.  The
+    first repetition warms up kernels and libraries and is not reported.
+    """
+    import numpy as np
+
+    from vlcache_amd import LLM, SamplingParams
+    from vlcache_amd.config import QWEN25_VL_3B
+
+    img_tok = QWEN25_VL_3B["image_token_id"]
+    llm = LLM(dict(QWEN25_VL_3B), recompute_ratio=ratio, num_kvcache_blocks=8 * 43, enforce_eager=True)
+    sp = SamplingParams(temperature=0.6, max_tokens=1)
+    grid = torch.tensor([[1, 154, 274]])
+    n_img = 77 * 137
+    rng = np.random.default_rng(0)
+
+    def prompt(prefix, suffix):
+        return ([int(x) for x in rng.integers(1, 150000, prefix)] + [img_tok] * n_img
+                + [int(x) for x in rng.integers(1, 150000, suffix)])
+
+    cold, warm = [], []
+    for r in range(reps + 1):
+        pv = torch.full((154 * 274, 1), float(r))  # a distinct image per repetition (only hashed)
+        mm = {"pixel_values": pv, "image_grid_thw": grid}
+        o1 = llm.generate([prompt(40, 64)], sp, mm_inputs=[mm])
+        o2 = llm.generate([prompt(128, 64)], sp, mm_inputs=[mm])
+        if r > 0:
+            cold.append(o1[0]["ttft"] * 1e3)
+            warm.append(o2[0]["ttft"] * 1e3)
+    del llm
+    torch.cuda.empty_cache()
+    return {"cold_ms": round(float(np.median(cold)), 2), "warm_ms": round(float(np.median(warm)), 2)}
+
+
 def run_cpu_baseline(hp, budget_s: float = 20.0):
     """The oracle (fp32 torch on the host CPU) on a bounded sample of the same workload."""
     from oracle import attention as oattn
@@ -166,7 +220,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="cfg2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ttft", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run one plain device-to-device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -177,6 +242,14 @@ def main():
 
     r = run_gpu(args.steps, args.warmup, args.workload)
     wl, hp = r["wl"], r["hp"]
+    ttft = None
+    if not args.no_ttft:
+        partial = run_ttft(wl.requests[0].ratio or 0.1)
+        full = run_ttft(0.0)
+        ttft = {"warm_partial_ms": partial["warm_ms"], "warm_full_recompute_ms": full["warm_ms"],
+                "cold_ms": partial["cold_ms"], "speedup_vs_full": round(full["warm_ms"] / partial["warm_ms"], 3),
+                "protocol": "cold (prefix 40) then warm (prefix 128) request, same 4K image, suffix 64, "
+                            "random-init 36-layer 3B, median of 2 after 1 warm-up"}
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(hp)
     frac = r["at_tflops"] / MFMA_BF16_PEAK_TFLOPS
     line = {
@@ -208,7 +281,7 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(frac, 4),
-            "traffic": None,
+            "traffic": _profiled_attention_traffic(args.workload),
         },
         "cpu_baseline": cpu,
         "kernels": {
@@ -222,6 +295,7 @@ def main():
                 "frac_hbm_peak": round(r["rr_gbps"] / HBM_PEAK_GBPS, 4)},
         },
         "ms_per_step_graph": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
+        "warm_ttft": ttft,
     }
     print(json.dumps(line), flush=True)
 
