@@ -28,13 +28,18 @@ namespace attn {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kKS = kHeadDim + 8;  // LDS row stride (bf16) of the K tile: 272 B, conflict-free b128 reads
-constexpr int kVS = kTileK + 4;    // LDS row stride (bf16) of the transposed V tile: 136 B
+// LDS row strides (bf16 elements).  K: 272 B, so the 16 rows a b128 operand read touches
+// fall in 16 distinct 16-byte bank slots.  V: 320 B (= 64 mod 256), so the 4 rows x 64 B a
+// half-wave's transpose reads touch fall in 8 distinct 32-byte bank slots.
+constexpr int kKS = kHeadDim + 8;
+constexpr int kVS = kHeadDim + 32;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 
 struct Params {
   const uint16_t* q;
@@ -84,7 +89,7 @@ constexpr float kRescaleThreshold = 8.0f;
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTileK * kKS];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kHeadDim * kVS];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kTileK * kVS];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -99,6 +104,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const int sq = p.cu_q[b + 1] - q0;
   const int k0 = p.cu_k[b];
   const int sk = p.cu_k[b + 1] - k0;
+
+  // Lane's element offset for the V^T operand transpose reads (ds_read_b64_tr_b16): in
+  // each 16-lane group, lane 4f + r reads 4 dims (4r..4r+3) of key row f, and the
+  // transpose hands lane j the 4 keys of dim j.  Group bit 0 picks the dim half,
+  // group bit 1 the key half (keys +4), matching the P^T operand's key order.
+  const int tr_off = (4 * hf + ((lane & 15) >> 2)) * kVS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   const int col = wave * 32 + lc;
   const int pos = col / p.group;
@@ -205,15 +216,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
     }
     return t;
   };
-  // Register -> LDS: K row-major, V transposed (two keys packed per 32-bit word).
-  // V rows with no valid key are zeroed here (K needs no zeroing: their scores are
-  // masked).  A tile whose block id is bad reads as all-zero V.
+  // Register -> LDS, both row-major (16-byte writes).  Rows of keys >= sk hold a
+  // copy of the tile's first row (the loads were redirected there); their V is
+  // zeroed so that P = 0 times V stays 0 whatever the cache holds, and K needs no
+  // zeroing because their scores are masked.  A tile whose block id is bad reads
+  // as all-zero V.
   auto store_tile = [&](TileRegs t, int kt) {
     bool clean = kt + kTileK <= sk;
     if (MODE == kPagedTiles) {
       const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + kt / p.page_size];
-      clean = clean && blk >= 0 && blk < p.num_blocks;
-      if (!(blk >= 0 && blk < p.num_blocks)) {
+      const bool ok = blk >= 0 && blk < p.num_blocks;
+      clean = clean && ok;
+      if (!ok) {
         const u32x4v z = {0u, 0u, 0u, 0u};
         t.va0 = z; t.vb0 = z; t.va1 = z; t.vb1 = z;
       }
@@ -237,18 +251,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
     *reinterpret_cast<u32x4v*>(k_lds + (r0 + 16) * kKS + dc * 8) = t.k1;
     *reinterpret_cast<u32x4v*>(k_lds + (r0 + 32) * kKS + dc * 8) = t.k2;
     *reinterpret_cast<u32x4v*>(k_lds + (r0 + 48) * kKS + dc * 8) = t.k3;
-    uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt_lds);
-    auto put = [&](int kp, const u32x4v& va, const u32x4v& vb) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t a = va[e], c = vb[e];
-        // d = dc*8 + 2e takes the low halves of both keys, d + 1 the high halves.
-        vt32[((dc * 8 + 2 * e) * kVS + 2 * kp) >> 1] = (a & 0xffffu) | (c << 16);
-        vt32[((dc * 8 + 2 * e + 1) * kVS + 2 * kp) >> 1] = (a >> 16) | (c & 0xffff0000u);
-      }
-    };
-    put(r0, t.va0, t.vb0);
-    put(r0 + 16, t.va1, t.vb1);
+    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0) * kVS + dc * 8) = t.va0;
+    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0 + 1) * kVS + dc * 8) = t.vb0;
+    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0 + 32) * kVS + dc * 8) = t.va1;
+    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0 + 33) * kVS + dc * 8) = t.vb1;
   };
 
   TileRegs next;
@@ -327,18 +333,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
         pk[kb][c] = __builtin_bit_cast(bf16x8, w);
       }
 
-    // ---- O^T += V^T P^T: lane supplies V^T[d][keys 16c+4hf+0..3, 16c+8+4hf+0..3] ----
+    // ---- O^T += V^T P^T: lane supplies V^T[d = 32mb + lane%32][keys base+4hf+0..3, base+8+4hf+0..3] ----
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
-      const uint16_t* vr = vt_lds + (mb * 32 + lc) * kVS + 4 * hf;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const int base = kb * 32 + 16 * c;
-          const u32x2v lo = *reinterpret_cast<const u32x2v*>(vr + base);
-          const u32x2v hi = *reinterpret_cast<const u32x2v*>(vr + base + 8);
-          const u32x4v w = {lo[0], lo[1], hi[0], hi[1]};
+          const uint16_t* vr = v_lds + (kb * 32 + 16 * c) * kVS + 32 * mb + tr_off;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(vr));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(vr + 8 * kVS));
+          const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pk[kb][c],
                                                           o[mb], 0, 0, 0);
         }
