@@ -28,11 +28,6 @@ namespace attn {
 namespace {
 
 constexpr int kThreads = 256;
-// LDS row strides (bf16 elements).  K: 272 B, so the 16 rows a b128 operand read touches
-// fall in 16 distinct 16-byte bank slots.  V: 320 B (= 64 mod 256), so the 4 rows x 64 B a
-// half-wave's transpose reads touch fall in 8 distinct 32-byte bank slots.
-constexpr int kKS = kHeadDim + 8;
-constexpr int kVS = kHeadDim + 32;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -75,6 +70,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Physical row of key `key` of sequence b through the block table, or -1 when the
+// key is past the sequence or its block id is outside the cache.
+__device__ __forceinline__ int64_t paged_row_of(const Params& p, int b, int sk, int key) {
+  const int kc = min(key, sk - 1);
+  const int pg = kc / p.page_size;
+  const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];
+  const bool ok = key < sk && blk >= 0 && blk < p.num_blocks;
+  return ok ? (int64_t)blk * p.page_size + (kc - pg * p.page_size) : -1;
+}
+
 // How keys map to rows of k/v.
 enum KvMode {
   kContiguous = 0,  // key j of sequence b is row cu_k[b] + j
@@ -86,13 +91,28 @@ enum KvMode {
 // max exceeds it by more than this, so P stays <= 2^8 and O is rarely rescaled.
 constexpr float kRescaleThreshold = 8.0f;
 
+// XOR swizzle of the 16-byte chunks of a 256-byte LDS row: chunk c of row r lives in
+// slot c ^ swz(r).  swz is a bijection on r mod 16 (so the 16 rows of a b128 operand
+// read hit 16 distinct slots) whose high two bits follow r mod 4 (so the 4 rows x 4
+// chunks of a half-wave's transpose reads also hit 16 distinct slots).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// All-zero rows: the source of keys past the end of a sequence and of pages whose
+// block id is outside the cache (they read as zeros).
+__device__ __attribute__((aligned(256))) const uint32_t kZeroRow[64] = {};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTileK * kKS];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kTileK * kVS];
+  // Two K and two V tile buffers (double buffering): 64 rows x 256 bytes each, swizzled.
+  __shared__ __attribute__((aligned(1024))) uint8_t k_buf0[kTileK * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_buf1[kTileK * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_buf0[kTileK * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_buf1[kTileK * 256];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lc = lane & 31;
   const int hf = lane >> 5;
@@ -104,12 +124,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const int sq = p.cu_q[b + 1] - q0;
   const int k0 = p.cu_k[b];
   const int sk = p.cu_k[b + 1] - k0;
-
-  // Lane's element offset for the V^T operand transpose reads (ds_read_b64_tr_b16): in
-  // each 16-lane group, lane 4f + r reads 4 dims (4r..4r+3) of key row f, and the
-  // transpose hands lane j the 4 keys of dim j.  Group bit 0 picks the dim half,
-  // group bit 1 the key half (keys +4), matching the P^T operand's key order.
-  const int tr_off = (4 * hf + ((lane & 15) >> 2)) * kVS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   const int col = wave * 32 + lc;
   const int pos = col / p.group;
@@ -134,6 +148,79 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
     }
   }
 
+  // ---- LDS read offsets (bytes, within a tile buffer) ---------------------------
+  // K operand of S^T: row kb*32 + lc, chunk 2kk + hf.
+  uint32_t koff[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) koff[kk] = lc * 256 + (((2 * kk + hf) ^ swz(lc)) << 4);
+  // V^T operand through ds_read_b64_tr_b16: in each 16-lane group, lane 4f + r reads
+  // dims 4r..4r+3 (of the group's 16-dim half) of key row f, and the transpose
+  // hands lane j the 4 keys of dim j.  Group bit 0 = dim half, bit 1 = key half
+  // (+4 keys); the second read of an operand is 8 keys further.
+  uint32_t voff[4][2];
+  {
+    const int s = lane & 15, grp = lane >> 4;
+    const int y = 2 * (grp & 1) + ((s & 3) >> 1);
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const int row = 4 * (grp >> 1) + (s >> 2) + 8 * rd;  // + kb*32 + 16c (multiple of 16)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        voff[mb][rd] = row * 256 + (((4 * mb + y) ^ swz(row)) << 4) + ((s & 1) << 3);
+    }
+  }
+
+  // ---- K/V tile loads straight into LDS (global_load_lds_dwordx4) --------------
+  // Wave w fills rows 16w .. 16w+15 of both tiles, 4 rows per instruction: lane i
+  // writes LDS slot i%16 of row 16w + 4j + i/16, so it loads that row's chunk
+  // (i%16) ^ swz(row).
+  const char* kcol = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim);
+  const char* vcol = reinterpret_cast<const char*>(p.v + (int64_t)g * kHeadDim);
+  const int64_t kst = p.k_row_stride * 2, vst = p.v_row_stride * 2;  // bytes
+  int lrow[4];
+  uint32_t lchunk[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    lrow[j] = 16 * wave + 4 * j + (lane >> 4);
+    lchunk[j] = (uint32_t)(((lane & 15) ^ swz(4 * j + (lane >> 4))) << 4);
+  }
+  const char* zero = reinterpret_cast<const char*>(kZeroRow);
+
+  auto issue_loads = [&](int kt, uint8_t* kdst, uint8_t* vdst) {
+    // Physical row of the tile's first key (kContiguous / kPagedTiles) and validity.
+    int64_t row0 = 0;
+    bool ok = true;
+    if (MODE == kContiguous) {
+      row0 = (int64_t)k0 + kt;
+    } else if (MODE == kPagedTiles) {
+      const int pg = kt / p.page_size;
+      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];  // uniform: scalar load
+      ok = blk >= 0 && blk < p.num_blocks;
+      row0 = (int64_t)blk * p.page_size + (kt - pg * p.page_size);
+    }
+    const bool full = ok && kt + kTileK <= sk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const char* ks;
+      const char* vs;
+      if (MODE == kPagedRows) {
+        const int64_t pr = paged_row_of(p, b, sk, kt + lrow[j]);
+        ks = pr >= 0 ? kcol + pr * kst + lchunk[j] : zero + lchunk[j];
+        vs = pr >= 0 ? vcol + pr * vst + lchunk[j] : zero + lchunk[j];
+      } else if (full) {
+        ks = kcol + (row0 + lrow[j]) * kst + lchunk[j];
+        vs = vcol + (row0 + lrow[j]) * vst + lchunk[j];
+      } else {
+        const bool rv = ok && kt + lrow[j] < sk;
+        ks = rv ? kcol + (row0 + lrow[j]) * kst + lchunk[j] : zero + lchunk[j];
+        vs = rv ? vcol + (row0 + lrow[j]) * vst + lchunk[j] : zero + lchunk[j];
+      }
+      const int lds_row = 16 * wave + 4 * j;
+      __builtin_amdgcn_global_load_lds(ks, (lds_void*)(kdst + lds_row * 256), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vs, (lds_void*)(vdst + lds_row * 256), 16, 0, 0);
+    }
+  };
+
   f32x16 o[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
@@ -142,145 +229,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   float mb_run = -INFINITY;  // running max, already scaled to log2 units
   float l = 0.f;
 
-  // ---- K/V tile staging -------------------------------------------------------
-  // A lane moves 16 bytes of 4 K rows (r0, r0+16, r0+32, r0+48) and of 4 V rows
-  // (key pairs r0 and r0+16) per 64-key tile.  For the contiguous and the
-  // page-aligned modes a tile is 64 consecutive rows from a uniform base, so the
-  // loads are "uniform pointer + per-lane 32-bit offset" with offsets computed
-  // once; rows past sk (only in the last tile) are redirected to the tile's first
-  // row and zeroed when the tile is written to LDS.
-  const int dc = tid & 15;
-  const int r0 = tid >> 4;
-  const int64_t kst = p.k_row_stride, vst = p.v_row_stride;
-  const char* kcol = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim + dc * 8);
-  const char* vcol = reinterpret_cast<const char*>(p.v + (int64_t)g * kHeadDim + dc * 8);
-  const uint32_t ko0 = (uint32_t)(r0 * kst * 2), ko1 = (uint32_t)((r0 + 16) * kst * 2),
-                 ko2 = (uint32_t)((r0 + 32) * kst * 2), ko3 = (uint32_t)((r0 + 48) * kst * 2);
-  const uint32_t vo0 = (uint32_t)(2 * r0 * vst * 2), vo1 = (uint32_t)((2 * r0 + 1) * vst * 2),
-                 vo2 = (uint32_t)((2 * r0 + 32) * vst * 2), vo3 = (uint32_t)((2 * r0 + 33) * vst * 2);
-
-  struct TileRegs {
-    u32x4v k0, k1, k2, k3;
-    u32x4v va0, vb0, va1, vb1;
-  };
-  auto ld16 = [](const char* base, uint32_t off) -> u32x4v {
-    return *reinterpret_cast<const u32x4v*>(base + off);
-  };
-  // Physical row of key `key` through the block table (generic page size), or -1.
-  auto paged_row = [&](int key) -> int64_t {
-    const int kc = min(key, sk - 1);
-    const int pg = kc / p.page_size;
-    const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];
-    const bool ok = key < sk && blk >= 0 && blk < p.num_blocks;
-    return ok ? (int64_t)blk * p.page_size + (kc - pg * p.page_size) : -1;
-  };
-  auto load_tile = [&](int kt) -> TileRegs {
-    TileRegs t;
-    if (MODE == kPagedRows) {
-      auto ld = [&](const char* col, int64_t st, int key) -> u32x4v {
-        const int64_t row = paged_row(key);
-        return ld16(col + (row >= 0 ? row : 0) * st * 2, 0u);
-      };
-      t.k0 = ld(kcol, kst, kt + r0);
-      t.k1 = ld(kcol, kst, kt + r0 + 16);
-      t.k2 = ld(kcol, kst, kt + r0 + 32);
-      t.k3 = ld(kcol, kst, kt + r0 + 48);
-      t.va0 = ld(vcol, vst, kt + 2 * r0);
-      t.vb0 = ld(vcol, vst, kt + 2 * r0 + 1);
-      t.va1 = ld(vcol, vst, kt + 2 * r0 + 32);
-      t.vb1 = ld(vcol, vst, kt + 2 * r0 + 33);
-      return t;
-    }
-    int64_t row0;
-    bool ok = true;
-    if (MODE == kContiguous) {
-      row0 = (int64_t)k0 + kt;
-    } else {
-      const int pg = kt / p.page_size;
-      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];  // uniform: scalar load
-      ok = blk >= 0 && blk < p.num_blocks;
-      row0 = ok ? (int64_t)blk * p.page_size + (kt - pg * p.page_size) : 0;
-    }
-    const char* kb = kcol + row0 * kst * 2;
-    const char* vb = vcol + row0 * vst * 2;
-    if (ok && kt + kTileK <= sk) {
-      t.k0 = ld16(kb, ko0); t.k1 = ld16(kb, ko1); t.k2 = ld16(kb, ko2); t.k3 = ld16(kb, ko3);
-      t.va0 = ld16(vb, vo0); t.vb0 = ld16(vb, vo1); t.va1 = ld16(vb, vo2); t.vb1 = ld16(vb, vo3);
-    } else {  // last (partial) tile or a bad block id: stay inside the tile's valid rows
-      const int nvalid = ok ? sk - kt : 1;
-      auto o = [&](uint32_t off, int r) { return r < nvalid ? off : 0u; };
-      t.k0 = ld16(kb, o(ko0, r0)); t.k1 = ld16(kb, o(ko1, r0 + 16));
-      t.k2 = ld16(kb, o(ko2, r0 + 32)); t.k3 = ld16(kb, o(ko3, r0 + 48));
-      t.va0 = ld16(vb, o(vo0, 2 * r0)); t.vb0 = ld16(vb, o(vo1, 2 * r0 + 1));
-      t.va1 = ld16(vb, o(vo2, 2 * r0 + 32)); t.vb1 = ld16(vb, o(vo3, 2 * r0 + 33));
-    }
-    return t;
-  };
-  // Register -> LDS, both row-major (16-byte writes).  Rows of keys >= sk hold a
-  // copy of the tile's first row (the loads were redirected there); their V is
-  // zeroed so that P = 0 times V stays 0 whatever the cache holds, and K needs no
-  // zeroing because their scores are masked.  A tile whose block id is bad reads
-  // as all-zero V.
-  auto store_tile = [&](TileRegs t, int kt) {
-    bool clean = kt + kTileK <= sk;
-    if (MODE == kPagedTiles) {
-      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + kt / p.page_size];
-      const bool ok = blk >= 0 && blk < p.num_blocks;
-      clean = clean && ok;
-      if (!ok) {
-        const u32x4v z = {0u, 0u, 0u, 0u};
-        t.va0 = z; t.vb0 = z; t.va1 = z; t.vb1 = z;
-      }
-    }
-    if (MODE != kPagedRows && !clean) {
-      const u32x4v z = {0u, 0u, 0u, 0u};
-      const int n = sk - kt;
-      if (2 * r0 >= n) t.va0 = z;
-      if (2 * r0 + 1 >= n) t.vb0 = z;
-      if (2 * r0 + 32 >= n) t.va1 = z;
-      if (2 * r0 + 33 >= n) t.vb1 = z;
-    }
-    if (MODE == kPagedRows) {  // rows that resolved to no cache row read row 0: zero them
-      const u32x4v z = {0u, 0u, 0u, 0u};
-      if (paged_row(kt + 2 * r0) < 0) t.va0 = z;
-      if (paged_row(kt + 2 * r0 + 1) < 0) t.vb0 = z;
-      if (paged_row(kt + 2 * r0 + 32) < 0) t.va1 = z;
-      if (paged_row(kt + 2 * r0 + 33) < 0) t.vb1 = z;
-    }
-    *reinterpret_cast<u32x4v*>(k_lds + (r0) * kKS + dc * 8) = t.k0;
-    *reinterpret_cast<u32x4v*>(k_lds + (r0 + 16) * kKS + dc * 8) = t.k1;
-    *reinterpret_cast<u32x4v*>(k_lds + (r0 + 32) * kKS + dc * 8) = t.k2;
-    *reinterpret_cast<u32x4v*>(k_lds + (r0 + 48) * kKS + dc * 8) = t.k3;
-    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0) * kVS + dc * 8) = t.va0;
-    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0 + 1) * kVS + dc * 8) = t.vb0;
-    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0 + 32) * kVS + dc * 8) = t.va1;
-    *reinterpret_cast<u32x4v*>(v_lds + (2 * r0 + 33) * kVS + dc * 8) = t.vb1;
-  };
-
-  TileRegs next;
-  if (k_begin < k_end) next = load_tile(k_begin);
-  for (int kt = k_begin; kt < k_end; kt += kTileK) {
-    __syncthreads();  // every wave is done reading the previous tile
-    store_tile(next, kt);
-    __syncthreads();
-    // Prefetch the following tile: its loads are in flight during this tile's math.
-    if (kt + kTileK < k_end) next = load_tile(kt + kTileK);
-
-    // ---- S^T = K Q^T for two 32-key blocks ----
+  // ---- one 64-key tile from LDS: S^T, mask, online softmax, O^T += V^T P^T ----
+  auto compute = [&](int kt, const uint8_t* kb_lds, const uint8_t* vb_lds) {
     f32x16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-      const uint16_t* kr = k_lds + (kb * 32 + lc) * kKS + 8 * hf;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(kr + 16 * kk);
+    for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(kb_lds + kb * 32 * 256 + koff[kk]);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[kb], 0, 0, 0);
       }
     }
-
-    // ---- mask: element e = 4i + j of block kb is key kt + 32kb + 8i + 4hf + j ----
+    // mask: element e = 4i + j of block kb is key kt + 32kb + 8i + 4hf + j
     if ((kt + kTileK - 1 > blk_min_limit) || (kt + kTileK > k_end)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -290,8 +254,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
           if (key > limit || key >= k_end) s[kb][e] = -INFINITY;
         }
     }
-
-    // ---- online softmax (lane = column; the two half-waves share the max) ----
+    // online softmax (lane = column; the two half-waves share the max)
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -320,8 +283,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
         rs += pe;
       }
     l += rs;
-
-    // ---- P^T as bf16 B operands: chunk c of block kb = elements 8c..8c+7 ----
+    // P^T as bf16 B operands: chunk c of block kb = elements 8c..8c+7
     bf16x8 pk[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -332,24 +294,39 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
         for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(s[kb][8 * c + 2 * t], s[kb][8 * c + 2 * t + 1]);
         pk[kb][c] = __builtin_bit_cast(bf16x8, w);
       }
-
-    // ---- O^T += V^T P^T: lane supplies V^T[d = 32mb + lane%32][keys base+4hf+0..3, base+8+4hf+0..3] ----
+    // O^T += V^T P^T
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint16_t* vr = v_lds + (kb * 32 + 16 * c) * kVS + 32 * mb + tr_off;
+        for (int mb = 0; mb < 4; ++mb) {
+          const uint8_t* vr = vb_lds + (kb * 32 + 16 * c) * 256;
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(vr));
+              (__attribute__((address_space(3))) s16x4*)(vr + voff[mb][0]));
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(vr + 8 * kVS));
+              (__attribute__((address_space(3))) s16x4*)(vr + voff[mb][1]));
           const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pk[kb][c],
                                                           o[mb], 0, 0, 0);
         }
-    }
+  };
+
+  // ---- main loop: two tiles per iteration so each buffer is a static array ----
+  // Order per tile: wait for this wave's loads of the tile, barrier (all loads of the
+  // tile landed; every wave is done with the other buffer), start the next tile's
+  // loads into the other buffer, compute.
+  if (k_begin < k_end) issue_loads(k_begin, k_buf0, v_buf0);
+  for (int kt = k_begin; kt < k_end; kt += 2 * kTileK) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+    if (kt + kTileK < k_end) issue_loads(kt + kTileK, k_buf1, v_buf1);
+    compute(kt, k_buf0, v_buf0);
+    if (kt + kTileK >= k_end) break;
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    if (kt + 2 * kTileK < k_end) issue_loads(kt + 2 * kTileK, k_buf0, v_buf0);
+    compute(kt + kTileK, k_buf1, v_buf1);
   }
 
   // ---- epilogue: lane holds O^T[d = 32mb + 8i + 4hf + j][col] in o[mb][4i + j] ----
