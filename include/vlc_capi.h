@@ -92,7 +92,8 @@ int vlc_rerotate_copy_kv(void* kv_cache, int64_t plane_stride, int64_t layer_str
  *
  * cu_seqlens_q/k: HOST int32 [num_seqs + 1] (the values prepare_prefill builds,
  *   engine/model_runner.py:197-198,256-259,284-285).
- * num_cus: compute units to plan for (256 on MI355X; <= 0 selects 256).
+ * num_cus: compute units to plan for (256 on MI355X; 0 selects 256); a negative
+ *   value plans one work item per query tile with no split of the key range.
  * Writes the plan into plan[0 .. *plan_len) (int32); returns VLC_ERR_CAPACITY
  * with *plan_len set to the required length when plan_capacity is too small.
  * *workspace_bytes receives the device workspace the plan needs.
@@ -119,7 +120,8 @@ int vlc_attn_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
  *   cu_seqlens_k[b] + j of k/v, at k_row_stride / v_row_stride elements.
  * causal: row i of a sequence with lengths (sq, sk) sees keys j <= i + sk - sq
  *   (bottom-right alignment); rows that see no key produce zeros.
- * cu_seqlens_q/k: DEVICE int32 [num_seqs + 1].
+ * cu_seqlens_q/k: DEVICE int32 [num_seqs + 1] holding the boundaries the plan was
+ *   built from, or NULL: the plan carries every boundary the kernels read.
  * plan_host / plan_dev: the plan from vlc_attn_plan, in host memory and as a
  *   device copy; plan_len its length.
  * workspace: device scratch of at least the planned workspace_bytes.

@@ -50,8 +50,8 @@ def test_status_strings(lib):
 def _items(plan):
     h = plan.host
     n_items, n_comb = int(h[1]), int(h[2])
-    items = h[16:16 + 8 * n_items].reshape(-1, 8)
-    comb = h[16 + 8 * n_items:16 + 8 * (n_items + n_comb)].reshape(-1, 8)
+    items = h[16:16 + 16 * n_items].reshape(-1, 16)
+    comb = h[16 + 16 * n_items:16 + 16 * (n_items + n_comb)].reshape(-1, 16)
     return items, comb
 
 
@@ -74,6 +74,7 @@ def _check_plan_covers(cu_q, cu_k, hq, hkv, causal, num_cus):
     slots_seen = []
     for it in items:
         b, g, qs, qc, kb, ke, slot = (int(x) for x in it[:7])
+        assert tuple(int(x) for x in it[7:11]) == (cu_q[b], cu_q[b + 1] - cu_q[b], cu_k[b], cu_k[b + 1] - cu_k[b])
         assert expect[(b, g, qs)][0] == qc
         got.setdefault((b, g, qs), []).append((kb, ke, slot))
         assert kb % 64 == 0 and kb <= ke

@@ -43,10 +43,17 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
   const int group = num_heads_q / num_heads_kv;
   if (group > kCols) return VLC_ERR_UNSUPPORTED;
   const int ppt = kCols / group;
+  const bool allow_split = num_cus >= 0;  // num_cus < 0: one item per query tile, no split-KV
   if (num_cus <= 0) num_cus = 256;
 
   struct Tile {
     int b, g, qs, qc, kmax, nkt;
+  };
+  auto bounds = [&](int32_t* v, int b) {
+    v[7] = cu_q[b];
+    v[8] = cu_q[b + 1] - cu_q[b];
+    v[9] = cu_k[b];
+    v[10] = cu_k[b + 1] - cu_k[b];
   };
   std::vector<Tile> tiles;
   int64_t total = 0;
@@ -78,10 +85,12 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
   for (const Tile& t : tiles) {
     // Round to the nearest number of chunks: a range up to 1.5 chunks stays whole.
     int nsplit = (int)std::min<int64_t>(kMaxSplits, std::max<int64_t>(1, (2 * t.nkt + chunk) / (2 * chunk)));
+    if (!allow_split) nsplit = 1;
     if (nsplit <= 1) {
       Item it{};
       it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;
-      it.v[4] = 0; it.v[5] = t.kmax; it.v[6] = -1; it.v[7] = 0;
+      it.v[4] = 0; it.v[5] = t.kmax; it.v[6] = -1;
+      bounds(it.v, t.b);
       it.cost = std::max(t.nkt, 1);
       items.push_back(it);
       continue;
@@ -90,6 +99,7 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
     nsplit = (t.nkt + per - 1) / per;
     Item c{};
     c.v[0] = t.b; c.v[1] = t.g; c.v[2] = t.qs; c.v[3] = t.qc; c.v[4] = next_slot; c.v[5] = nsplit;
+    bounds(c.v, t.b);
     c.cost = nsplit;
     combines.push_back(c);
     for (int s = 0; s < nsplit; ++s) {
@@ -97,7 +107,8 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
       const int kb = s * per * kTileK;
       const int ke = std::min(t.kmax, (s + 1) * per * kTileK);
       it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;
-      it.v[4] = kb; it.v[5] = ke; it.v[6] = next_slot + s; it.v[7] = 0;
+      it.v[4] = kb; it.v[5] = ke; it.v[6] = next_slot + s;
+      bounds(it.v, t.b);
       it.cost = (ke - kb + kTileK - 1) / kTileK;
       items.push_back(it);
     }

@@ -9,7 +9,7 @@ namespace attn {
 constexpr int kHeadDim = 128;   // only head_dim supported by the MFMA kernel
 constexpr int kTileK = 64;      // keys per LDS tile; split boundaries are multiples of it
 constexpr int kCols = 128;      // (query position, q head) columns per workgroup
-constexpr int kItemInts = 8;    // int32 per work item / combine item
+constexpr int kItemInts = 16;   // int32 per work item / combine item (64 bytes, one scalar load)
 constexpr int kHeaderInts = 16; // int32 plan header
 constexpr int32_t kPlanMagic = 0x564c4331;  // "VLC1"
 constexpr int kMinChunkTiles = 4;           // smallest split: 4 key tiles = 256 keys
@@ -30,15 +30,17 @@ enum PlanField {
   kPHeadDim = 10,
 };
 
-// Work item (int32 x 8): one workgroup.
+// Work item (int32 x 16): one workgroup.
 //   [0] seq  [1] kv_head  [2] q_start  [3] q_count  [4] k_begin  [5] k_end
-//   [6] partial slot (-1 = write the normalised output)  [7] unused
-// Combine item (int32 x 8): merges the partial slots of one query tile.
+//   [6] partial slot (-1 = write the normalised output)
+//   [7] q0 = cu_seqlens_q[seq]  [8] sq  [9] k0 = cu_seqlens_k[seq]  [10] sk  [11..15] unused
+// Combine item (int32 x 16): merges the partial slots of one query tile.
 //   [0] seq  [1] kv_head  [2] q_start  [3] q_count  [4] first slot  [5] num splits
-//   [6..7] unused
+//   [7] q0  [8] sq  [9] k0  [10] sk  [6, 11..15] unused
+// Carrying the sequence bounds in the item saves the kernels a dependent load.
 
-// Bytes of workspace per partial slot: fp32 O [kCols][kHeadDim] + fp32 (m, l) [kCols].
-constexpr int64_t kSlotBytes = (int64_t)kCols * kHeadDim * 4 + (int64_t)kCols * 2 * 4;
+// Bytes of workspace per partial slot: bf16 O/l [kCols][kHeadDim] + fp32 (m, l) [kCols].
+constexpr int64_t kSlotBytes = (int64_t)kCols * kHeadDim * 2 + (int64_t)kCols * 2 * 4;
 
 }  // namespace attn
 }  // namespace vlc

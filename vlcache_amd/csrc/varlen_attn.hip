@@ -46,8 +46,8 @@ struct Params {
   const int32_t* items;
   const int32_t* combine;
   uint16_t* out;
-  float* part_o;   // [slots][kCols][kHeadDim]
-  float* part_ml;  // [slots][kCols][2]  (m * scale * log2e, l)
+  uint16_t* part_o;  // [slots][kCols][kHeadDim] bf16: the split's own normalised output O_s / l_s
+  float* part_ml;    // [slots][kCols][2] fp32: (m_s in scaled log2 units, l_s)
   int64_t q_row_stride;
   int64_t k_row_stride;
   int64_t v_row_stride;
@@ -61,6 +61,7 @@ struct Params {
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -120,10 +121,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const int32_t* it = p.items + (int64_t)blockIdx.x * kItemInts;
   const int b = it[0], g = it[1], q_start = it[2], q_count = it[3];
   const int k_begin = it[4], k_end = it[5], slot = it[6];
-  const int q0 = p.cu_q[b];
-  const int sq = p.cu_q[b + 1] - q0;
-  const int k0 = p.cu_k[b];
-  const int sk = p.cu_k[b + 1] - k0;
+  const int q0 = it[7], sq = it[8], k0 = it[9], sk = it[10];
 
   const int col = wave * 32 + lc;
   const int pos = col / p.group;
@@ -177,13 +175,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const char* kcol = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim);
   const char* vcol = reinterpret_cast<const char*>(p.v + (int64_t)g * kHeadDim);
   const int64_t kst = p.k_row_stride * 2, vst = p.v_row_stride * 2;  // bytes
-  int lrow[4];
-  uint32_t lchunk[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    lrow[j] = 16 * wave + 4 * j + (lane >> 4);
-    lchunk[j] = (uint32_t)(((lane & 15) ^ swz(4 * j + (lane >> 4))) << 4);
-  }
+  // Row 16w + 4j + (lane >> 4) of the tile, chunk (lane & 15) ^ swz(4j + (lane >> 4))
+  // = ((lane & 15) ^ ((lane >> 4) << 2)) ^ j: both recomputed per load from one value.
+  const int lrow0 = 16 * wave + (lane >> 4);
+  const uint32_t lchunk0 = (uint32_t)((lane & 15) ^ ((lane >> 4) << 2));
   const char* zero = reinterpret_cast<const char*>(kZeroRow);
 
   auto issue_loads = [&](int kt, uint8_t* kdst, uint8_t* vdst) {
@@ -201,19 +196,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
     const bool full = ok && kt + kTileK <= sk;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int lrow_j = lrow0 + 4 * j;
+      const uint32_t lchunk_j = (lchunk0 ^ (uint32_t)j) << 4;
       const char* ks;
       const char* vs;
       if (MODE == kPagedRows) {
-        const int64_t pr = paged_row_of(p, b, sk, kt + lrow[j]);
-        ks = pr >= 0 ? kcol + pr * kst + lchunk[j] : zero + lchunk[j];
-        vs = pr >= 0 ? vcol + pr * vst + lchunk[j] : zero + lchunk[j];
+        const int64_t pr = paged_row_of(p, b, sk, kt + lrow_j);
+        ks = pr >= 0 ? kcol + pr * kst + lchunk_j : zero + lchunk_j;
+        vs = pr >= 0 ? vcol + pr * vst + lchunk_j : zero + lchunk_j;
       } else if (full) {
-        ks = kcol + (row0 + lrow[j]) * kst + lchunk[j];
-        vs = vcol + (row0 + lrow[j]) * vst + lchunk[j];
+        ks = kcol + (row0 + lrow_j) * kst + lchunk_j;
+        vs = vcol + (row0 + lrow_j) * vst + lchunk_j;
       } else {
-        const bool rv = ok && kt + lrow[j] < sk;
-        ks = rv ? kcol + (row0 + lrow[j]) * kst + lchunk[j] : zero + lchunk[j];
-        vs = rv ? vcol + (row0 + lrow[j]) * vst + lchunk[j] : zero + lchunk[j];
+        const bool rv = ok && kt + lrow_j < sk;
+        ks = rv ? kcol + (row0 + lrow_j) * kst + lchunk_j : zero + lchunk_j;
+        vs = rv ? vcol + (row0 + lrow_j) * vst + lchunk_j : zero + lchunk_j;
       }
       const int lds_row = 16 * wave + 4 * j;
       __builtin_amdgcn_global_load_lds(ks, (lds_void*)(kdst + lds_row * 256), 16, 0, 0);
@@ -346,14 +343,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
         *reinterpret_cast<u32x2v*>(orow + d) = w;
       }
   } else {
-    float* po = p.part_o + ((int64_t)slot * kCols + col) * kHeadDim;
+    // Split of a longer key range: the normalised partial in bf16 plus (m, l) in fp32.
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    uint16_t* po = p.part_o + ((int64_t)slot * kCols + col) * kHeadDim;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = 32 * mb + 8 * i + 4 * hf;
-        float4 w = make_float4(o[mb][4 * i], o[mb][4 * i + 1], o[mb][4 * i + 2], o[mb][4 * i + 3]);
-        *reinterpret_cast<float4*>(po + d) = w;
+        u32x2v w;
+        w[0] = pack_bf16x2(o[mb][4 * i] * inv, o[mb][4 * i + 1] * inv);
+        w[1] = pack_bf16x2(o[mb][4 * i + 2] * inv, o[mb][4 * i + 3] * inv);
+        *reinterpret_cast<u32x2v*>(po + d) = w;
       }
     if (hf == 0) {
       float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
@@ -364,50 +365,52 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
 }
 
 // Merge the split-KV partials of one query tile:
-//   O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,  M = max_s m_s.
-// grid = (combine items, kCols / kCombineCols): a workgroup owns kCombineCols
-// columns; each lane owns one 4-float slice of one column's output row, so
-// the split loop's loads are independent and overlap.
-constexpr int kCombineCols = kThreads / (kHeadDim / 4);  // 8 columns per workgroup
+//   O = sum_s 2^(m_s - M) l_s Ohat_s / sum_s 2^(m_s - M) l_s,  M = max_s m_s,
+// with Ohat_s = O_s / l_s stored in bf16.  grid = (combine items, kCols /
+// kCombineCols): a workgroup owns kCombineCols columns and each lane one 8-dim
+// (16-byte) slice of a column, so the loads of the split loop are independent.
+constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 16 columns per workgroup
 
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) {
   const int32_t* it = p.combine + (int64_t)blockIdx.x * kItemInts;
-  const int b = it[0], g = it[1], q_start = it[2], q_count = it[3];
+  const int g = it[1], q_start = it[2], q_count = it[3];
   const int first = it[4], nsplit = it[5];
-  const int col = blockIdx.y * kCombineCols + threadIdx.x / (kHeadDim / 4);
-  const int d = 4 * (threadIdx.x % (kHeadDim / 4));
+  const int q0 = it[7];
+  const int col = blockIdx.y * kCombineCols + threadIdx.x / (kHeadDim / 8);
+  const int d = 8 * (threadIdx.x % (kHeadDim / 8));
   const int pos = col / p.group;
   if (pos >= q_count) return;
   const int hh = col - pos * p.group;
   const float* ml = p.part_ml + ((int64_t)first * kCols + col) * 2;
-  const float* po = p.part_o + ((int64_t)first * kCols + col) * kHeadDim + d;
+  const uint16_t* po = p.part_o + ((int64_t)first * kCols + col) * kHeadDim + d;
   const int64_t ml_stride = (int64_t)kCols * 2;
   const int64_t po_stride = (int64_t)kCols * kHeadDim;
   float mmax = -INFINITY;
 #pragma unroll 8
   for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, ml[s * ml_stride]);
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
   if (mmax != -INFINITY) {
 #pragma unroll 4
     for (int s = 0; s < nsplit; ++s) {
       const float2 mls = *reinterpret_cast<const float2*>(ml + s * ml_stride);
-      const float4 v = *reinterpret_cast<const float4*>(po + s * po_stride);
-      const float w = fast_exp2(mls.x - mmax);
-      lsum += w * mls.y;
-      acc.x += w * v.x;
-      acc.y += w * v.y;
-      acc.z += w * v.z;
-      acc.w += w * v.w;
+      const u32x4v v = *reinterpret_cast<const u32x4v*>(po + s * po_stride);
+      const float wl = fast_exp2(mls.x - mmax) * mls.y;
+      lsum += wl;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[2 * t] += wl * bf16_bits_to_f32(v[t] & 0xffffu);
+        acc[2 * t + 1] += wl * bf16_bits_to_f32(v[t] >> 16);
+      }
     }
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  uint16_t* orow = p.out + (int64_t)(p.cu_q[b] + q_start + pos) * p.out_row_stride +
+  uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
                    (int64_t)(g * p.group + hh) * kHeadDim + d;
-  u32x2v w;
-  w[0] = pack_bf16x2(acc.x * inv, acc.y * inv);
-  w[1] = pack_bf16x2(acc.z * inv, acc.w * inv);
-  *reinterpret_cast<u32x2v*>(orow) = w;
+  u32x4v w;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
+  *reinterpret_cast<u32x4v*>(orow) = w;
 }
 
 }  // namespace
@@ -437,7 +440,7 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   const int64_t n_items = h[kPNumItems], n_comb = h[kPNumCombine], n_slots = h[kPNumSlots];
   if (plan_len < kHeaderInts + (n_items + n_comb) * kItemInts) return VLC_ERR_PLAN;
   if (n_items == 0) return VLC_OK;
-  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k) return VLC_ERR_INVALID;
+  if (!q || !k || !v || !out) return VLC_ERR_INVALID;
   if (!(softmax_scale > 0.f)) return VLC_ERR_INVALID;
   // 16-byte vector access of every row.
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || q_row_stride % 8 ||
@@ -460,9 +463,9 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   prm.items = plan_dev + kHeaderInts;
   prm.combine = plan_dev + kHeaderInts + n_items * kItemInts;
   prm.out = static_cast<uint16_t*>(out);
-  prm.part_o = static_cast<float*>(workspace);
+  prm.part_o = static_cast<uint16_t*>(workspace);
   prm.part_ml = n_slots > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                        n_slots * (int64_t)kCols * kHeadDim * 4)
+                                                        n_slots * (int64_t)kCols * kHeadDim * 2)
                             : nullptr;
   prm.q_row_stride = q_row_stride;
   prm.k_row_stride = k_row_stride;
