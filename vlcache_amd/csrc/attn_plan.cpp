@@ -73,8 +73,8 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
     }
   }
 
-  // Split long key ranges so that roughly two workgroups per CU have work.
-  const int64_t target_blocks = 2LL * num_cus;
+  // Split long key ranges so that every resident workgroup slot has work.
+  const int64_t target_blocks = (int64_t)kBlocksPerCU * num_cus;
   int64_t chunk = (total + target_blocks - 1) / std::max<int64_t>(1, target_blocks);
   chunk = std::max<int64_t>(chunk, kMinChunkTiles);
 
@@ -86,6 +86,9 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
     // Round to the nearest number of chunks: a range up to 1.5 chunks stays whole.
     int nsplit = (int)std::min<int64_t>(kMaxSplits, std::max<int64_t>(1, (2 * t.nkt + chunk) / (2 * chunk)));
     if (!allow_split) nsplit = 1;
+    // No item longer than kMaxItemTiles key tiles.
+    nsplit = std::max(nsplit, (t.nkt + kMaxItemTiles - 1) / kMaxItemTiles);
+    if (nsplit > kMaxSplits) return VLC_ERR_UNSUPPORTED;
     if (nsplit <= 1) {
       Item it{};
       it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;

@@ -9,11 +9,13 @@ namespace attn {
 constexpr int kHeadDim = 128;   // only head_dim supported by the MFMA kernel
 constexpr int kTileK = 64;      // keys per LDS tile; split boundaries are multiples of it
 constexpr int kCols = 128;      // (query position, q head) columns per workgroup
+constexpr int kBlocksPerCU = 2; // attention workgroups resident per CU
 constexpr int kItemInts = 16;   // int32 per work item / combine item (64 bytes, one scalar load)
 constexpr int kHeaderInts = 16; // int32 plan header
 constexpr int32_t kPlanMagic = 0x564c4331;  // "VLC1"
 constexpr int kMinChunkTiles = 4;           // smallest split: 4 key tiles = 256 keys
 constexpr int kMaxSplits = 256;
+constexpr int kMaxItemTiles = 1024;        // key tiles per work item (the kernel's page-id table)
 
 // Plan header fields (int32 offsets).
 enum PlanField {

@@ -4,22 +4,31 @@
 //
 // Work decomposition (built on the host by vlc_attn_plan): a workgroup of four
 // wave64s owns one work item = (sequence, kv head, tile of query positions,
-// key range).  Its 128 "columns" are (query position, q head) pairs: the
-// `group` q heads that share the kv head are packed side by side, so one K/V
-// tile staged in LDS feeds every head of the group.
+// key range); two workgroups share a CU.  Its 128 "columns" are (query
+// position, q head) pairs: the `group` q heads that share the kv head are
+// packed side by side, so one K/V tile staged in LDS feeds every head of the
+// group.
 //
 // Per 64-key tile each wave computes S^T = K * Q^T (keys x its 32 columns) with
 // v_mfma_f32_32x32x16_bf16.  In that orientation a lane owns ONE column and 16
 // keys of each 32-key block, so the softmax row reductions are lane-local plus
 // a single exchange between the two half-waves.  The probabilities P^T are
 // already in the B-operand layout of the second product O^T += V^T P^T, so they
-// never leave registers; V is transposed into LDS when it is staged.
+// never leave registers; V stays row-major in LDS and is read transposed
+// (ds_read_b64_tr_b16).
+//
+// The tile loop is software-pipelined inside each wave: step t issues the PV
+// product of tile t-1 and the QK product of tile t+1 on the matrix pipe while
+// the VALU runs the softmax of tile t, with the instruction order fixed by hand.
+// K/V tiles go global -> LDS by DMA (global_load_lds_dwordx4), two tiles ahead.
 //
 // Online softmax in fp32 with exp2 (the softmax scale and log2(e) are folded
-// into one multiply-add), P rounded to bf16 for the PV product, O accumulated
-// in fp32 and normalised once at the end.  Items whose key range was split
-// write unnormalised O with (m, l) to a workspace slot; attn_combine merges
-// the slots of a query tile.
+// into one multiply-add) and a lazy running max, P rounded to bf16 for the PV
+// product, O accumulated in fp32 and normalised once at the end.  Items whose
+// key range was split write their normalised O (bf16) with (m, l) to a
+// workspace slot; attn_combine merges the slots of a query tile.
+#include <type_traits>
+
 #include "attn_plan.h"
 #include "common.h"
 
@@ -27,7 +36,7 @@ namespace vlc {
 namespace attn {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;  // four wave64s, one per SIMD
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -104,13 +113,67 @@ __device__ __attribute__((aligned(256))) const uint32_t kZeroRow[64] = {};
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// ---- LDS-DMA and barriers ----------------------------------------------------
+// Tile loads go global -> LDS with global_load_lds_dwordx4 (lane i's 16 bytes land
+// at M0 + 16 i).  They are issued through inline assembly: the compiler's model
+// of an LDS DMA in flight is a flat access of unknown order, which would force
+// every later LDS read wait to drain the whole queue (lgkmcnt(0)) and break the
+// operand pipeline of the products.  The hardware counts these loads in vmcnt
+// only, and every read of a loaded buffer is preceded by sync_tiles(), which waits
+// for vmcnt(0) and is a compiler memory barrier, so no LDS value is cached across
+// it.
+__device__ __forceinline__ uint32_t lds_u32(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const lds_void*)ptr;
+}
+// Uniform base + per-lane 32-bit offset.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "m0");
+}
+// Per-lane 64-bit address.
+__device__ __forceinline__ void dma16_addr(const void* addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(addr)
+               : "m0");
+}
+// Every tile load of this wave has landed, every LDS access of this wave is done,
+// then the workgroup barrier.
+__device__ __forceinline__ void sync_tiles() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One work item = (sequence, kv head, kCols = 128 columns, key range): four waves,
+// one per SIMD, each owning 32 columns; two workgroups share a CU.
+//
+// Software pipeline over key tiles: step t runs, in one instruction stream,
+//   O^T += V^T P^T of tile t-1   (16 MFMAs, V tile t-1 from LDS)
+//   S^T  = K Q^T  of tile t+1    (16 MFMAs, K tile t+1 from LDS)
+//   softmax of tile t            (VALU: max, exp2, sum, bf16 pack)
+// which are independent, so the VALU work issues while the matrix pipe is busy.
+// The rescale of O by the softmax of tile t waits until the products of tile
+// t-1 are in.  During step t the loads of K tile t+2 and V tile t fill the
+// buffers that step t-1 read.
+// max(x) over lanes l and l ^ 32.  v_permlane32_swap exchanges the upper half of
+// its first operand with the lower half of its second; with both operands x the
+// two results hold, in every lane, the lane's own x and its partner's.  A VALU
+// operation, so the softmax that depends on it does not wait behind the LDS reads
+// of the products (as ds_bpermute would).
+__device__ __forceinline__ float half_wave_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
-  // Two K and two V tile buffers (double buffering): 64 rows x 256 bytes each, swizzled.
+__global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_buf0[kTileK * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t k_buf1[kTileK * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t v_buf0[kTileK * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t v_buf1[kTileK * 256];
+  __shared__ int32_t tile_blk[kMaxItemTiles];  // kPagedTiles: block id of each key tile
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -122,7 +185,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const int b = it[0], g = it[1], q_start = it[2], q_count = it[3];
   const int k_begin = it[4], k_end = it[5], slot = it[6];
   const int q0 = it[7], sq = it[8], k0 = it[9], sk = it[10];
+  const int n_tiles = (k_end - k_begin + kTileK - 1) / kTileK;
 
+  // ---- the lane's column: wave*32 + lc ----------------------------------------------
   const int col = wave * 32 + lc;
   const int pos = col / p.group;
   const int hh = col - pos * p.group;
@@ -130,7 +195,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   const int qpos = q_start + pos;
   const int head = g * p.group + hh;
   const int limit = p.causal ? qpos + sk - sq : sk - 1;             // last visible key
-  const int blk_min_limit = p.causal ? q_start + sk - sq : sk - 1;  // smallest limit in the block
+  const int blk_min_limit = p.causal ? q_start + sk - sq : sk - 1;  // smallest limit in the item
+  const int last_key = min(blk_min_limit, k_end - 1);              // keys <= last_key need no mask
+  // Leading tiles that need no mask.
+  const int n_plain = max(0, min(n_tiles, (last_key - k_begin + 1) / kTileK));
 
   // Q^T fragment (B operand of S^T = K Q^T): lane holds Q[col][16*kk + 8*hf .. +8].
   // Invalid columns load row 0 (always readable) and are zeroed.
@@ -147,220 +215,381 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
   }
 
   // ---- LDS read offsets (bytes, within a tile buffer) ---------------------------
-  // K operand of S^T: row kb*32 + lc, chunk 2kk + hf.
-  uint32_t koff[8];
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk) koff[kk] = lc * 256 + (((2 * kk + hf) ^ swz(lc)) << 4);
+  // K operand of S^T: row kb*32 + lc, chunk 2kk + hf, i.e. byte offset
+  // koff0 ^ (kk << 5) (the chunk field is bits 4..7 and 2kk, hf are disjoint bits).
+  const uint32_t koff0 = lc * 256 + ((hf ^ swz(lc)) << 4);
+  // Lane offsets are recomputed from an opaque copy of their base where they are
+  // used (an XOR or a multiply-add each) rather than hoisted out of the tile loop
+  // as live registers: registers are the limit of this kernel.
+  auto opaque = [](uint32_t x) __attribute__((always_inline)) {
+    asm volatile("" : "+v"(x));
+    return x;
+  };
   // V^T operand through ds_read_b64_tr_b16: in each 16-lane group, lane 4f + r reads
   // dims 4r..4r+3 (of the group's 16-dim half) of key row f, and the transpose
   // hands lane j the 4 keys of dim j.  Group bit 0 = dim half, bit 1 = key half
-  // (+4 keys); the second read of an operand is 8 keys further.
-  uint32_t voff[4][2];
+  // (+4 keys); the second read of an operand is 8 keys further.  Dim block mb
+  // XORs chunk bits (mb << 2) and +8 keys XORs row bit 3 and chunk bit 1 (swz of
+  // row + 8 is swz(row) ^ 2), so every offset is voff0 ^ a constant.
+  uint32_t voff0;
   {
-    const int s = lane & 15, grp = lane >> 4;
-    const int y = 2 * (grp & 1) + ((s & 3) >> 1);
-#pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-      const int row = 4 * (grp >> 1) + (s >> 2) + 8 * rd;  // + kb*32 + 16c (multiple of 16)
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        voff[mb][rd] = row * 256 + (((4 * mb + y) ^ swz(row)) << 4) + ((s & 1) << 3);
-    }
+    const int s = lane & 15, lg = lane >> 4;
+    const int y = 2 * (lg & 1) + ((s & 3) >> 1);
+    const int row = 4 * (lg >> 1) + (s >> 2);  // + 8rd + kb*32 + 16c
+    voff0 = row * 256 + ((y ^ swz(row)) << 4) + ((s & 1) << 3);
   }
 
-  // ---- K/V tile loads straight into LDS (global_load_lds_dwordx4) --------------
-  // Wave w fills rows 16w .. 16w+15 of both tiles, 4 rows per instruction: lane i
-  // writes LDS slot i%16 of row 16w + 4j + i/16, so it loads that row's chunk
-  // (i%16) ^ swz(row).
+
+  // ---- tile loads: wave w fills rows 16w .. 16w+15, 4 rows per instruction -----
+  // Lane i writes LDS slot i%16 of row 16w + 4j + i/16, so it loads that row's
+  // chunk (i%16) ^ swz(row) = (i%16) ^ ((i/16) << 2) ^ j.
   const char* kcol = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim);
   const char* vcol = reinterpret_cast<const char*>(p.v + (int64_t)g * kHeadDim);
   const int64_t kst = p.k_row_stride * 2, vst = p.v_row_stride * 2;  // bytes
-  // Row 16w + 4j + (lane >> 4) of the tile, chunk (lane & 15) ^ swz(4j + (lane >> 4))
-  // = ((lane & 15) ^ ((lane >> 4) << 2)) ^ j: both recomputed per load from one value.
-  const int lrow0 = 16 * wave + (lane >> 4);
+  const uint32_t lrow0 = 16 * wave + (lane >> 4);
   const uint32_t lchunk0 = (uint32_t)((lane & 15) ^ ((lane >> 4) << 2));
   const char* zero = reinterpret_cast<const char*>(kZeroRow);
 
-  auto issue_loads = [&](int kt, uint8_t* kdst, uint8_t* vdst) {
-    // Physical row of the tile's first key (kContiguous / kPagedTiles) and validity.
-    int64_t row0 = 0;
-    bool ok = true;
+  // Loads tile u of the item into an LDS buffer, without a branch: tiles past the
+  // item and pages outside the cache read the zero row; rows past the sequence
+  // read its last row (their keys are masked, so the products never use them).
+  auto dma_tile = [&](int u, uint8_t* dst, const char* colbase, int64_t st) __attribute__((always_inline)) {
+    const int kt = k_begin + u * kTileK;
+    const uint32_t lr = opaque(lrow0), lcn = opaque(lchunk0);
+    if (MODE == kPagedRows) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int lrow = (int)lr + 4 * j;
+        const uint32_t lchunk = (lcn ^ (uint32_t)j) << 4;
+        const int64_t pr = u < n_tiles ? paged_row_of(p, b, sk, kt + lrow) : -1;
+        const char* src = pr >= 0 ? colbase + pr * st + lchunk : zero + lchunk;
+        dma16_addr(src, lds_u32(dst + (16 * wave + 4 * j) * 256));
+      }
+      return;
+    }
+    const bool in = u < n_tiles;
+    int64_t row0;
+    bool ok = in;
     if (MODE == kContiguous) {
       row0 = (int64_t)k0 + kt;
-    } else if (MODE == kPagedTiles) {
-      const int pg = kt / p.page_size;
-      const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];  // uniform: scalar load
-      ok = blk >= 0 && blk < p.num_blocks;
-      row0 = (int64_t)blk * p.page_size + (kt - pg * p.page_size);
+    } else {
+      const int32_t blk = __builtin_amdgcn_readfirstlane(tile_blk[min(u, max(n_tiles - 1, 0))]);
+      ok = ok && blk >= 0 && blk < p.num_blocks;
+      row0 = (int64_t)blk * p.page_size + (kt % p.page_size);
     }
-    const bool full = ok && kt + kTileK <= sk;
+    const char* tb = ok ? colbase + row0 * st : zero;
+    const uint32_t last = ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u;  // last row to read
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int lrow_j = lrow0 + 4 * j;
-      const uint32_t lchunk_j = (lchunk0 ^ (uint32_t)j) << 4;
-      const char* ks;
-      const char* vs;
-      if (MODE == kPagedRows) {
-        const int64_t pr = paged_row_of(p, b, sk, kt + lrow_j);
-        ks = pr >= 0 ? kcol + pr * kst + lchunk_j : zero + lchunk_j;
-        vs = pr >= 0 ? vcol + pr * vst + lchunk_j : zero + lchunk_j;
-      } else if (full) {
-        ks = kcol + (row0 + lrow_j) * kst + lchunk_j;
-        vs = vcol + (row0 + lrow_j) * vst + lchunk_j;
-      } else {
-        const bool rv = ok && kt + lrow_j < sk;
-        ks = rv ? kcol + (row0 + lrow_j) * kst + lchunk_j : zero + lchunk_j;
-        vs = rv ? vcol + (row0 + lrow_j) * vst + lchunk_j : zero + lchunk_j;
-      }
-      const int lds_row = 16 * wave + 4 * j;
-      __builtin_amdgcn_global_load_lds(ks, (lds_void*)(kdst + lds_row * 256), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vs, (lds_void*)(vdst + lds_row * 256), 16, 0, 0);
-    }
+    for (int j = 0; j < 4; ++j)
+      dma16(tb, min(lr + 4 * j, last) * (uint32_t)st + ((lcn ^ (uint32_t)j) << 4),
+            lds_u32(dst + (16 * wave + 4 * j) * 256));
   };
 
+  // ---- state ---------------------------------------------------------------------
   f32x16 o[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[mb][e] = 0.f;
-  float mb_run = -INFINITY;  // running max, already scaled to log2 units
-  float l = 0.f;
+  f32x16 s_even[2], s_odd[2];        // S^T of even / odd tiles: [key block]
+  bf16x8 pk[2][2];                   // P^T between its softmax and its product: [key block][chunk]
+  float m_run = -INFINITY;           // running max, scaled to log2 units
+  float l_run = 0.f;
 
-  // ---- one 64-key tile from LDS: S^T, mask, online softmax, O^T += V^T P^T ----
-  auto compute = [&](int kt, const uint8_t* kb_lds, const uint8_t* vb_lds) {
-    f32x16 s[2];
+  // S^T = K Q^T of one tile (K from LDS): 16 operand reads, 16 MFMAs.
+  auto qk = [&](const uint8_t* kb_lds, f32x16 (&S)[2]) __attribute__((always_inline)) {
+    const uint32_t kof = opaque(koff0);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+      for (int e = 0; e < 16; ++e) S[kb][e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(kb_lds + kb * 32 * 256 + koff[kk]);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[kb], 0, 0, 0);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(kb_lds + kb * 32 * 256 + (kof ^ (kk << 5)));
+        S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], S[kb], 0, 0, 0);
       }
+  };
+  // Instruction order hint for the products of the prologue (sched groups: 0x008
+  // MFMA, 0x100 LDS read): operand reads run a few MFMAs ahead of their use.
+  auto order_qk = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    // mask: element e = 4i + j of block kb is key kt + 32kb + 8i + 4hf + j
-    if ((kt + kTileK - 1 > blk_min_limit) || (kt + kTileK > k_end)) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kt + kb * 32 + 8 * (e >> 2) + 4 * hf + (e & 3);
-          if (key > limit || key >= k_end) s[kb][e] = -INFINITY;
-        }
-    }
-    // online softmax (lane = column; the two half-waves share the max)
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.scale_log2;
-    const bool grow = mx > mb_run + kRescaleThreshold;
-    if (__builtin_amdgcn_ballot_w64(grow)) {  // rare after the first tile
-      const float mb_new = grow ? mx : mb_run;
-      const float alpha = grow ? fast_exp2(mb_run - mb_new) : 1.f;  // first growth: 2^-inf = 0
-      mb_run = mb_new;
-      l *= alpha;
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  };
+  auto rescale = [&](float alpha) __attribute__((always_inline)) {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[mb][e] *= alpha;
     }
-    const float m_base = (mb_run == -INFINITY) ? 0.f : mb_run;
-    float rs = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pe = fast_exp2(__builtin_fmaf(s[kb][e], p.scale_log2, -m_base));
-        s[kb][e] = pe;
-        rs += pe;
-      }
-    l += rs;
-    // P^T as bf16 B operands: chunk c of block kb = elements 8c..8c+7
-    bf16x8 pk[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        u32x4v w;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(s[kb][8 * c + 2 * t], s[kb][8 * c + 2 * t + 1]);
-        pk[kb][c] = __builtin_bit_cast(bf16x8, w);
-      }
-    // O^T += V^T P^T
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const uint8_t* vr = vb_lds + (kb * 32 + 16 * c) * 256;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(vr + voff[mb][0]));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(vr + voff[mb][1]));
-          const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pk[kb][c],
-                                                          o[mb], 0, 0, 0);
-        }
   };
 
-  // ---- main loop: two tiles per iteration so each buffer is a static array ----
-  // Order per tile: wait for this wave's loads of the tile, barrier (all loads of the
-  // tile landed; every wave is done with the other buffer), start the next tile's
-  // loads into the other buffer, compute.
-  if (k_begin < k_end) issue_loads(k_begin, k_buf0, v_buf0);
-  for (int kt = k_begin; kt < k_end; kt += 2 * kTileK) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __syncthreads();
-    if (kt + kTileK < k_end) issue_loads(kt + kTileK, k_buf1, v_buf1);
-    compute(kt, k_buf0, v_buf0);
-    if (kt + kTileK >= k_end) break;
-    __builtin_amdgcn_s_waitcnt(0x0f70);
-    __syncthreads();
-    if (kt + 2 * kTileK < k_end) issue_loads(kt + 2 * kTileK, k_buf0, v_buf0);
-    compute(kt + kTileK, k_buf1, v_buf1);
+  // Sources of one tile load: a uniform base and the last row to read (see dma_tile).
+  struct DmaSrc {
+    const char* base;
+    uint32_t last;
+  };
+  // direct: read the block id from the block table (scalar load) instead of the
+  // LDS copy, for the prologue, which does not wait for that copy.
+  auto dma_src = [&](int u, const char* colbase, int64_t st, bool direct = false) __attribute__((always_inline)) {
+    const int kt = k_begin + u * kTileK;
+    int64_t row0;
+    bool ok = u < n_tiles;
+    if (MODE == kContiguous) {
+      row0 = (int64_t)k0 + kt;
+    } else {
+      typedef const __attribute__((address_space(4))) int32_t* const_i32p;
+      const int32_t blk =
+          direct ? (ok ? ((const_i32p)(uintptr_t)(p.block_table + (int64_t)b * p.bt_row_stride))[kt / p.page_size] : 0)
+                 : __builtin_amdgcn_readfirstlane(tile_blk[min(u, max(n_tiles - 1, 0))]);
+      ok = ok && blk >= 0 && blk < p.num_blocks;
+      row0 = (int64_t)blk * p.page_size + (kt % p.page_size);
+    }
+    return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u};
+  };
+
+  // O^T += V^T P^T of the last tile, reads kAhead MFMAs ahead (sched groups: 0x008
+  // MFMA, 0x100 LDS read).
+  auto pv_last = [&](const uint8_t* v_rd) __attribute__((always_inline)) {
+    const uint32_t vof = opaque(voff0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint8_t* vr = v_rd + ((j >> 3) * 32 + 16 * ((j >> 2) & 1)) * 256;
+      const uint32_t mb = (uint32_t)(j & 3) << 6;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ mb)));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ (mb | 32u | 2048u))));
+      const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pk[j >> 3][(j >> 2) & 1],
+                                                         o[j & 3], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 13; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+  };
+
+  // One step t with explicit buffers and S registers: K tile t+1 and V tile t-1
+  // are read from buffer (t+1)&1, K tile t+2 and V tile t are loaded into buffer
+  // t&1.  The step is straight-line code: at t = 0 the products read a zeroed V
+  // buffer with P = 0, at t = n-1 they compute an S^T that is never used and load
+  // zero rows.
+  //
+  // Its instruction order is fixed by hand, in 32 units separated by
+  // sched_barrier: unit i issues MFMA i (PV for i < 16, QK after), the operand
+  // read of MFMA i + kAhead, one tile load (units 0..7) and a slice of the
+  // softmax of tile t (mask and max in units 0..2, the new running max in unit
+  // 3, one or two exp2 per unit after), so the VALU work fills the matrix pipe's
+  // shadow.  P^T of tile t-1 is read by the PV MFMAs before the softmax packs the
+  // new one after the last unit.
+  auto step_body = [&](auto masked, int t, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], uint8_t* k_rd, uint8_t* v_rd,
+                       uint8_t* k_ld, uint8_t* v_ld) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked)::value;
+    constexpr int kAhead = 3;
+    const int kt = k_begin + t * kTileK;
+    const DmaSrc dk = dma_src(t + 2, kcol, kst), dv = dma_src(t, vcol, vst);
+    const uint32_t kof = opaque(koff0), vof = opaque(voff0);
+    const uint32_t lr = opaque(lrow0), lcn = opaque(lchunk0);
+    const int rel = min(limit, k_end - 1) - kt - 4 * hf;  // MASKED: keys past rel are masked
+
+    bf16x8 op[32];
+    auto read_op = [&](int j) __attribute__((always_inline)) {
+      if (j < 16) {  // V^T operand: key block j >> 3, 16-key chunk (j >> 2) & 1, dim block j & 3
+        const uint8_t* vr = v_rd + ((j >> 3) * 32 + 16 * ((j >> 2) & 1)) * 256;
+        const uint32_t mb = (uint32_t)(j & 3) << 6;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ mb)));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ (mb | 32u | 2048u))));
+        const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        op[j] = __builtin_bit_cast(bf16x8, w);
+      } else {  // K operand: head-dim step (j - 16) >> 1, key block (j - 16) & 1
+        const int kk = (j - 16) >> 1, kb = (j - 16) & 1;
+        op[j] = *reinterpret_cast<const bf16x8*>(k_rd + kb * 32 * 256 + (kof ^ (uint32_t)(kk << 5)));
+      }
+    };
+    auto mfma_op = [&](int j) __attribute__((always_inline)) {
+      if (j < 16) {
+        const int mb = j & 3;
+        o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[j], pk[j >> 3][(j >> 2) & 1], o[mb], 0, 0, 0);
+      } else {
+        const int kk = (j - 16) >> 1, kb = (j - 16) & 1;
+        const f32x16 zacc = {};
+        s_nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[j], qf[kk], kk == 0 ? zacc : s_nxt[kb], 0, 0, 0);
+      }
+    };
+    // element n = 0..31 of the tile for this lane: key block n >> 4, element n & 15
+    auto get = [&](int n) __attribute__((always_inline)) { return s_cur[n >> 4][n & 15]; };
+    auto set = [&](int n, float v) __attribute__((always_inline)) { s_cur[n >> 4][n & 15] = v; };
+    float mxp[3] = {-INFINITY, -INFINITY, -INFINITY};
+    float alpha = 1.f, m_base = 0.f, rs = 0.f;
+    // An empty asm that takes a value in a register: the computation of the value
+    // stays before it (the compiler would otherwise sink the softmax past the
+    // barrier at the end of the step, next to its consumers).
+    auto pin = [](float& x) __attribute__((always_inline)) { asm volatile("" : "+v"(x)); };
+    auto exp_elem = [&](int n) __attribute__((always_inline)) {
+      float pe = fast_exp2(__builtin_fmaf(get(n), p.scale_log2, -m_base));
+      pin(pe);
+      set(n, pe);
+      rs += pe;
+    };
+
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) read_op(j);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (i + kAhead < 32) read_op(i + kAhead);
+      mfma_op(i);
+      if (MODE != kPagedRows) {
+        if (i < 4) {
+          dma16(dk.base, min(lr + 4 * i, dk.last) * (uint32_t)kst + ((lcn ^ (uint32_t)i) << 4),
+                lds_u32(k_ld + (16 * wave + 4 * i) * 256));
+        } else if (i < 8) {
+          const int r = i - 4;
+          dma16(dv.base, min(lr + 4 * r, dv.last) * (uint32_t)vst + ((lcn ^ (uint32_t)r) << 4),
+                lds_u32(v_ld + (16 * wave + 4 * r) * 256));
+        }
+      } else {
+        if (i == 0) dma_tile(t + 2, k_ld, kcol, kst);
+        if (i == 1) dma_tile(t, v_ld, vcol, vst);
+      }
+      if (i < 3) {  // mask and partial max of elements 11i .. 11i+10
+#pragma unroll
+        for (int n = 11 * i; n < min(32, 11 * i + 11); ++n) {
+          if (MASKED) {
+            // element n is key kt + 32(n >> 4) + 8((n & 15) >> 2) + 4hf + (n & 3)
+            if (32 * (n >> 4) + 8 * ((n & 15) >> 2) + (n & 3) > rel) set(n, -INFINITY);
+          }
+          mxp[i] = fmaxf(mxp[i], get(n));
+        }
+        pin(mxp[i]);
+      } else if (i == 3) {
+        // Lazy rescale: the running max moves only when the tile's max exceeds it
+        // by more than kRescaleThreshold; O and l are zero until the first move.
+        const float mx = half_wave_max(fmaxf(fmaxf(mxp[0], mxp[1]), mxp[2])) * p.scale_log2;
+        const bool grow = mx > m_run + kRescaleThreshold;
+        const float m_new = grow ? mx : m_run;
+        alpha = (grow && m_run != -INFINITY) ? fast_exp2(m_run - m_new) : 1.f;
+        m_run = m_new;
+        m_base = (m_new == -INFINITY) ? 0.f : m_new;
+        pin(m_base);
+        pin(alpha);
+      } else if (i < 8) {  // two elements per unit, then one
+        exp_elem(2 * (i - 4));
+        exp_elem(2 * (i - 4) + 1);
+      } else {
+        exp_elem(i);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_run = l_run * alpha + rs;
+    // P^T as bf16 B operands: chunk ch of key block kb = elements 8ch .. 8ch+7
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        u32x4v w;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = pack_bf16x2(s_cur[kb][8 * ch + 2 * u], s_cur[kb][8 * ch + 2 * u + 1]);
+        pk[kb][ch] = __builtin_bit_cast(bf16x8, w);
+        asm volatile("" : "+v"(pk[kb][ch]));
+      }
+    asm volatile("" : "+v"(l_run), "+v"(m_run));
+    rescale(alpha);
+    sync_tiles();
+  };
+  auto step = [&](auto par, auto masked, int t) __attribute__((always_inline)) {
+    if constexpr (decltype(par)::value != 0)
+      step_body(masked, t, s_odd, s_even, k_buf0, v_buf0, k_buf1, v_buf1);
+    else
+      step_body(masked, t, s_even, s_odd, k_buf1, v_buf1, k_buf0, v_buf0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using Masked = std::integral_constant<bool, true>;
+  using Plain = std::integral_constant<bool, false>;
+
+  // ---- prologue: V buffer 1 zeroed, K tiles 0 and 1, S^T of tile 0 ----------------
+  if (n_tiles > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4v*>(v_buf1 + (i * kThreads + tid) * 16) = u32x4v{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) pk[kb][ch] = __builtin_bit_cast(bf16x8, u32x4v{0u, 0u, 0u, 0u});
+    if (MODE == kPagedRows) {
+      dma_tile(0, k_buf0, kcol, kst);
+      dma_tile(1, k_buf1, kcol, kst);
+    } else {
+      const DmaSrc d0 = dma_src(0, kcol, kst, true), d1 = dma_src(1, kcol, kst, true);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t off = ((lchunk0 ^ (uint32_t)j) << 4);
+        dma16(d0.base, min(lrow0 + 4 * j, d0.last) * (uint32_t)kst + off, lds_u32(k_buf0 + (16 * wave + 4 * j) * 256));
+        dma16(d1.base, min(lrow0 + 4 * j, d1.last) * (uint32_t)kst + off, lds_u32(k_buf1 + (16 * wave + 4 * j) * 256));
+      }
+    }
+    // Paged: block ids of the item's tiles, read once into LDS (the steps take them
+    // from there); the barrier below publishes them.
+    if (MODE == kPagedTiles) {
+      for (int i = tid; i < n_tiles; i += kThreads)
+        tile_blk[i] = p.block_table[(int64_t)b * p.bt_row_stride + (k_begin + i * kTileK) / p.page_size];
+    }
+    sync_tiles();
+    qk(k_buf0, s_even);
+    order_qk();
+    sync_tiles();  // K buffer 0 is reloaded during step 0
+
+    // ---- steps: unmasked pairs, masked pairs, a masked single step if n is odd ---
+    int t = 0;
+    for (; t + 1 < n_plain; t += 2) {
+      step(I0{}, Plain{}, t);
+      step(I1{}, Plain{}, t + 1);
+    }
+    for (; t + 1 < n_tiles; t += 2) {
+      step(I0{}, Masked{}, t);
+      step(I1{}, Masked{}, t + 1);
+    }
+    if (t < n_tiles) step(I0{}, Masked{}, t);  // t is even here
+    // ---- drain: O^T += V^T P^T of the last tile ---------------------------------------
+    if ((n_tiles - 1) & 1) pv_last(v_buf1);
+    else pv_last(v_buf0);
   }
 
   // ---- epilogue: lane holds O^T[d = 32mb + 8i + 4hf + j][col] in o[mb][4i + j] ----
-  const float l_tot = l + __shfl_xor(l, 32);
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (!valid) return;
-  if (slot < 0) {
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    uint16_t* orow = p.out + (int64_t)(q0 + qpos) * p.out_row_stride + (int64_t)head * kHeadDim;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  // A split of a longer key range writes its normalised partial in bf16 plus
+  // (m, l) in fp32 to its workspace slot.
+  uint16_t* orow = slot < 0 ? p.out + (int64_t)(q0 + qpos) * p.out_row_stride + (int64_t)head * kHeadDim
+                            : p.part_o + ((int64_t)slot * kCols + col) * kHeadDim;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * mb + 8 * i + 4 * hf;
-        u32x2v w;
-        w[0] = pack_bf16x2(o[mb][4 * i] * inv, o[mb][4 * i + 1] * inv);
-        w[1] = pack_bf16x2(o[mb][4 * i + 2] * inv, o[mb][4 * i + 3] * inv);
-        *reinterpret_cast<u32x2v*>(orow + d) = w;
-      }
-  } else {
-    // Split of a longer key range: the normalised partial in bf16 plus (m, l) in fp32.
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    uint16_t* po = p.part_o + ((int64_t)slot * kCols + col) * kHeadDim;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * mb + 8 * i + 4 * hf;
-        u32x2v w;
-        w[0] = pack_bf16x2(o[mb][4 * i] * inv, o[mb][4 * i + 1] * inv);
-        w[1] = pack_bf16x2(o[mb][4 * i + 2] * inv, o[mb][4 * i + 3] * inv);
-        *reinterpret_cast<u32x2v*>(po + d) = w;
-      }
-    if (hf == 0) {
-      float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
-      ml[0] = mb_run;
-      ml[1] = l_tot;
+    for (int i = 0; i < 4; ++i) {
+      const int d = 32 * mb + 8 * i + 4 * hf;
+      u32x2v w;
+      w[0] = pack_bf16x2(o[mb][4 * i] * inv, o[mb][4 * i + 1] * inv);
+      w[1] = pack_bf16x2(o[mb][4 * i + 2] * inv, o[mb][4 * i + 3] * inv);
+      *reinterpret_cast<u32x2v*>(orow + d) = w;
     }
+  if (slot >= 0 && hf == 0) {
+    float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
+    ml[0] = m_run;
+    ml[1] = l_tot;
   }
 }
 
@@ -369,7 +598,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const Params p) {
 // with Ohat_s = O_s / l_s stored in bf16.  grid = (combine items, kCols /
 // kCombineCols): a workgroup owns kCombineCols columns and each lane one 8-dim
 // (16-byte) slice of a column, so the loads of the split loop are independent.
-constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 16 columns per workgroup
+constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 32 columns per workgroup
 
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) {
   const int32_t* it = p.combine + (int64_t)blockIdx.x * kItemInts;
@@ -440,6 +669,18 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   const int64_t n_items = h[kPNumItems], n_comb = h[kPNumCombine], n_slots = h[kPNumSlots];
   if (plan_len < kHeaderInts + (n_items + n_comb) * kItemInts) return VLC_ERR_PLAN;
   if (n_items == 0) return VLC_OK;
+  // The kernels index with the plan's fields: check them against the call.
+  for (int64_t i = 0; i < n_items + n_comb; ++i) {
+    const int32_t* v = h + kHeaderInts + i * kItemInts;
+    const bool is_item = i < n_items;
+    if (v[0] < 0 || v[0] >= num_seqs || v[1] < 0 || v[1] >= num_heads_kv || v[2] < 0 || v[3] < 0 ||
+        v[3] > kCols / group)
+      return VLC_ERR_PLAN;
+    if (is_item && (v[4] < 0 || v[5] < v[4] || (int64_t)v[5] - v[4] > (int64_t)kMaxItemTiles * kTileK ||
+                    v[6] >= n_slots || v[5] > v[10]))
+      return VLC_ERR_PLAN;
+    if (!is_item && (v[4] < 0 || v[5] < 1 || (int64_t)v[4] + v[5] > n_slots)) return VLC_ERR_PLAN;
+  }
   if (!q || !k || !v || !out) return VLC_ERR_INVALID;
   if (!(softmax_scale > 0.f)) return VLC_ERR_INVALID;
   // 16-byte vector access of every row.
