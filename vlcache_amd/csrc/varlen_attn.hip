@@ -597,42 +597,75 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 //   O = sum_s 2^(m_s - M) l_s Ohat_s / sum_s 2^(m_s - M) l_s,  M = max_s m_s,
 // with Ohat_s = O_s / l_s stored in bf16.  grid = (combine items, kCols /
 // kCombineCols): a workgroup owns kCombineCols columns and each lane one 8-dim
-// (16-byte) slice of a column, so the loads of the split loop are independent.
-constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 32 columns per workgroup
+// (16-byte) slice of a column.  The merge is latency-bound (a few KB per split),
+// so both passes keep many loads in flight: the 16 lanes of a column share the
+// (m, l) loads of the max and reduce it with shuffles, and the weighted sum is
+// unrolled 16 splits deep.
+constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 16 columns per workgroup
 
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) {
   const int32_t* it = p.combine + (int64_t)blockIdx.x * kItemInts;
   const int g = it[1], q_start = it[2], q_count = it[3];
   const int first = it[4], nsplit = it[5];
   const int q0 = it[7];
+  const int sub = threadIdx.x % (kHeadDim / 8);  // the lane's slice; lanes of a column are adjacent
   const int col = blockIdx.y * kCombineCols + threadIdx.x / (kHeadDim / 8);
-  const int d = 8 * (threadIdx.x % (kHeadDim / 8));
+  const int d = 8 * sub;
   const int pos = col / p.group;
-  if (pos >= q_count) return;
-  const int hh = col - pos * p.group;
+  const bool valid = pos < q_count;  // whole 16-lane groups agree (same column)
   const float* ml = p.part_ml + ((int64_t)first * kCols + col) * 2;
   const uint16_t* po = p.part_o + ((int64_t)first * kCols + col) * kHeadDim + d;
   const int64_t ml_stride = (int64_t)kCols * 2;
   const int64_t po_stride = (int64_t)kCols * kHeadDim;
+  // Loads are batched explicitly (indices clamped to the last split, extra terms
+  // weighted 0) so that a batch is in flight at once.
+  constexpr int kLanes = kHeadDim / 8;  // lanes per column
+  constexpr int kBatch = 16;
   float mmax = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, ml[s * ml_stride]);
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  if (mmax != -INFINITY) {
-#pragma unroll 4
-    for (int s = 0; s < nsplit; ++s) {
-      const float2 mls = *reinterpret_cast<const float2*>(ml + s * ml_stride);
-      const u32x4v v = *reinterpret_cast<const u32x4v*>(po + s * po_stride);
-      const float wl = fast_exp2(mls.x - mmax) * mls.y;
-      lsum += wl;
+  if (valid) {
+    for (int s0 = 0; s0 < nsplit; s0 += 4 * kLanes) {
+      float m4[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[2 * t] += wl * bf16_bits_to_f32(v[t] & 0xffffu);
-        acc[2 * t + 1] += wl * bf16_bits_to_f32(v[t] >> 16);
-      }
+      for (int k = 0; k < 4; ++k) m4[k] = ml[min(s0 + sub + k * kLanes, nsplit - 1) * ml_stride];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k]);
     }
   }
+#pragma unroll
+  for (int x = 1; x < kLanes; x <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, x));
+  if (!valid) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  auto merge = [&](auto batch) __attribute__((always_inline)) {
+    constexpr int B = decltype(batch)::value;
+    for (int s0 = 0; s0 < nsplit; s0 += B) {
+      float2 mls[B];
+      u32x4v v[B];
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const int s = min(s0 + k, nsplit - 1);
+        mls[k] = *reinterpret_cast<const float2*>(ml + s * ml_stride);
+        v[k] = *reinterpret_cast<const u32x4v*>(po + s * po_stride);
+      }
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const float wl = s0 + k < nsplit ? fast_exp2(mls[k].x - mmax) * mls[k].y : 0.f;
+        lsum += wl;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
+          acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
+        }
+      }
+    }
+  };
+  if (mmax != -INFINITY) {
+    // Batch depth by split count: deep batches for long merges, no wasted loads
+    // for short ones.
+    if (nsplit > 8) merge(std::integral_constant<int, kBatch>{});
+    else merge(std::integral_constant<int, 4>{});
+  }
+  const int hh = col - pos * p.group;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
                    (int64_t)(g * p.group + hh) * kHeadDim + d;
