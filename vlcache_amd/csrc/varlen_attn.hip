@@ -569,24 +569,41 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   }
 
   // ---- epilogue: lane holds O^T[d = 32mb + 8i + 4hf + j][col] in o[mb][4i + j] ----
+  // The wave's 32 columns are staged in LDS as bf16 rows of 256 bytes (16-byte
+  // chunk c of column x at slot c ^ (x & 15)) and then stored as whole rows, 16
+  // bytes per lane: the rows of the `group` heads of one position are adjacent in
+  // the output (and all rows of a workspace slot are), so each store instruction
+  // writes 1 KB of contiguous memory.  The K buffers are free here.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (!valid) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  // A split of a longer key range writes its normalised partial in bf16 plus
-  // (m, l) in fp32 to its workspace slot.
-  uint16_t* orow = slot < 0 ? p.out + (int64_t)(q0 + qpos) * p.out_row_stride + (int64_t)head * kHeadDim
-                            : p.part_o + ((int64_t)slot * kCols + col) * kHeadDim;
+  uint8_t* stage = (wave < 2 ? k_buf0 : k_buf1) + (wave & 1) * (kTileK * 256 / 2);
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int d = 32 * mb + 8 * i + 4 * hf;
       u32x2v w;
       w[0] = pack_bf16x2(o[mb][4 * i] * inv, o[mb][4 * i + 1] * inv);
       w[1] = pack_bf16x2(o[mb][4 * i + 2] * inv, o[mb][4 * i + 3] * inv);
-      *reinterpret_cast<u32x2v*>(orow + d) = w;
+      *reinterpret_cast<u32x2v*>(stage + lc * 256 + (((4 * mb + i) ^ (lc & 15)) << 4) + 8 * hf) = w;
     }
-  if (slot >= 0 && hf == 0) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's staging writes are done
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int x = 4 * r + (lane >> 4);  // column of the wave
+    const int ch = lane & 15;            // 16-byte chunk (dims 8ch .. 8ch+7)
+    const u32x4v v = *reinterpret_cast<const u32x4v*>(stage + x * 256 + ((ch ^ (x & 15)) << 4));
+    const int colx = wave * 32 + x;
+    const int posx = colx / p.group;
+    if (posx < q_count) {
+      // A split of a longer key range writes its normalised partial in bf16 plus
+      // (m, l) in fp32 to its workspace slot.
+      uint16_t* dst = slot < 0 ? p.out + (int64_t)(q0 + q_start + posx) * p.out_row_stride +
+                                     (int64_t)(g * p.group + colx - posx * p.group) * kHeadDim
+                               : p.part_o + ((int64_t)slot * kCols + colx) * kHeadDim;
+      *reinterpret_cast<u32x4v*>(dst + 8 * ch) = v;
+    }
+  }
+  if (slot >= 0 && valid && hf == 0) {
     float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
     ml[0] = m_run;
     ml[1] = l_tot;
