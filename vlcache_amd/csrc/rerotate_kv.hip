@@ -28,7 +28,8 @@ namespace vlc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUPT = 2;  // units per thread (unrolled by hand in the kernel)
+constexpr int kUPT = 4;  // units per thread
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void rotate_word(uint32_t& a, uint32_t& b, float2 cs0, float2 cs1) {
 #pragma clang fp contract(off)
@@ -84,8 +85,9 @@ __global__ __launch_bounds__(kThreads) void rerotate_copy_kv_kernel(
     if (os < 0 || os >= num_slots || ns < 0 || ns >= num_slots) return un;
     const int64_t off = (int64_t)hh * head_dim + 8 * j;
     const uint16_t* src = base + os * row_elems + off;
-    u32x4 lo = *reinterpret_cast<const u32x4*>(src);
-    u32x4 hi = *reinterpret_cast<const u32x4*>(src + half);
+    // Streaming data, touched once: nontemporal loads and stores.
+    u32x4 lo = __builtin_bit_cast(u32x4, __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src)));
+    u32x4 hi = __builtin_bit_cast(u32x4, __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src + half)));
     if (rot) {
       int sgi = seg_of_token ? seg_of_token[n] : 0;
       sgi = sgi < 0 ? 0 : (sgi >= num_segments ? num_segments - 1 : sgi);
@@ -101,17 +103,16 @@ __global__ __launch_bounds__(kThreads) void rerotate_copy_kv_kernel(
     return un;
   };
   for (int64_t u0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; u0 < total; u0 += stride * kUPT) {
-    // kUPT = 2 units: four 16-byte loads in flight before the first store.
-    const Unit a = fetch(u0);
-    const Unit c = fetch(u0 + stride);
-    if (a.dst) {
-      *reinterpret_cast<u32x4*>(a.dst) = a.lo;
-      *reinterpret_cast<u32x4*>(a.dst + half) = a.hi;
-    }
-    if (c.dst) {
-      *reinterpret_cast<u32x4*>(c.dst) = c.lo;
-      *reinterpret_cast<u32x4*>(c.dst + half) = c.hi;
-    }
+    // kUPT units: 2 * kUPT 16-byte loads in flight before the first store.
+    Unit un[kUPT];
+#pragma unroll
+    for (int k = 0; k < kUPT; ++k) un[k] = fetch(u0 + k * stride);
+#pragma unroll
+    for (int k = 0; k < kUPT; ++k)
+      if (un[k].dst) {
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, un[k].lo), reinterpret_cast<u32x4v*>(un[k].dst));
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, un[k].hi), reinterpret_cast<u32x4v*>(un[k].dst + half));
+      }
   }
 }
 
