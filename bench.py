@@ -8,12 +8,15 @@ image KV cached at text prefix 40 and re-rotated to prefix 128, paged KV in
 before the timed region.
 
 A step = the all-layer K-rerotate + V copy of the reused image KV, then for each
-of the 36 layers the KV scatter of the 1247 recomputed tokens and the varlen
-paged GQA causal attention of those tokens against the 10741-token cache.
+of the 36 layers the fused M-RoPE of the 1247 recomputed tokens' q and k with
+the store of their k and v into the paged cache, and the varlen paged GQA
+causal attention of those tokens against the 10741-token cache.
 
 value = attention microseconds per layer (mean over the timed steps, HIP
 events on the launch stream around each attention call: main kernel + split-KV
-combine).  The scatter bandwidth comes from the same events.  The rerotate is
+combine).  The fused RoPE + store time comes from the same events; the
+unfused sequence it replaces (torch eager RoPE, then the separate scatter) is
+timed after the step loop for comparison.  The rerotate is
 timed cold as well (a 512 MiB write evicts the MALL before each of 10 runs,
 median), next to a plain device copy of the same bytes timed the same way.
 """
@@ -86,7 +89,7 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
     torch.cuda.synchronize()
 
     ev_rr = _events(steps)
-    ev_sc = _events(steps * L)
+    ev_rs = _events(steps * L)
     ev_at = _events(steps * L)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -97,9 +100,9 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
             ev_rr[s][1].record()
         for layer in range(L):
             i = s * L + layer
-            ev_sc[i][0].record()
-            hp.scatter(layer)
-            ev_sc[i][1].record()
+            ev_rs[i][0].record()
+            hp.rope_store(layer)
+            ev_rs[i][1].record()
             ev_at[i][0].record()
             hp.attention(layer)
             ev_at[i][1].record()
@@ -127,10 +130,27 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
     except Exception as e:  # report, do not hide
         print(f"graph replay unavailable: {e!r}", file=sys.stderr)
 
+    # The unfused sequence the fused kernel replaces, timed the same way (warm):
+    # the reference's separate store_kvcache scatter, and torch's eager RoPE of q and k.
+    ev_sc = _events(steps * L)
+    ev_tr = _events(steps * L)
+    for s in range(steps):
+        for layer in range(L):
+            i = s * L + layer
+            ev_sc[i][0].record()
+            hp.scatter(layer)
+            ev_sc[i][1].record()
+            ev_tr[i][0].record()
+            hp.torch_rope()
+            ev_tr[i][1].record()
+    torch.cuda.synchronize()
+
     cu_q, cu_k = hp.cu_q_host, hp.cu_k_host
     flops = workloads.attention_flops(cu_q, cu_k, m.num_heads, m.head_dim)
     at_ms = _mean_ms(ev_at)
+    rs_ms = _mean_ms(ev_rs)
     sc_ms = _mean_ms(ev_sc)
+    tr_ms = _mean_ms(ev_tr)
     rr_ms = _mean_ms(ev_rr) if hp.n_reused else None
     rr_in_step_ms = rr_ms
     copy_ms = None
@@ -162,11 +182,14 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
     at_tflops = flops / (at_ms * 1e-3) / 1e12
     sc_bytes = workloads.scatter_bytes(hp.n_computed, m.num_kv_heads, m.head_dim)
     sc_gbps = sc_bytes / (sc_ms * 1e-3) / 1e9
+    rs_bytes = workloads.rope_store_bytes(hp.n_computed, m.num_heads, m.num_kv_heads, m.head_dim)
+    rs_gbps = rs_bytes / (rs_ms * 1e-3) / 1e9
     rr_bytes = workloads.rerotate_bytes(hp.n_reused, L, m.num_kv_heads, m.head_dim, with_v=True)
     rr_gbps = rr_bytes / (rr_ms * 1e-3) / 1e9 if rr_ms else None
     return dict(
         wl=wl, hp=hp, wall=wall, graph_ms=graph_ms, flops=flops,
         at_us=at_ms * 1e3, at_tflops=at_tflops, sc_us=sc_ms * 1e3, sc_gbps=sc_gbps, sc_bytes=sc_bytes,
+        rs_us=rs_ms * 1e3, rs_gbps=rs_gbps, rs_bytes=rs_bytes, torch_rope_us=tr_ms * 1e3,
         rr_us=rr_ms * 1e3 if rr_ms else None, rr_gbps=rr_gbps, rr_bytes=rr_bytes,
         rr_in_step_us=rr_in_step_ms * 1e3 if rr_in_step_ms else None,
         copy_gbps=rr_bytes / (copy_ms * 1e-3) / 1e9 if copy_ms else None,
@@ -319,8 +342,14 @@ def main():
             "attention": {"us_per_layer": round(r["at_us"], 3), "gflop_per_layer": round(r["flops"] / 1e9, 3),
                           "tflops": round(r["at_tflops"], 2), "frac_mfma_peak": round(frac, 4),
                           "work_items": r["plan"][0], "split_combines": r["plan"][1]},
+            "rope_store": {"us_per_layer": round(r["rs_us"], 3), "bytes": r["rs_bytes"],
+                           "gbps": round(r["rs_gbps"], 1), "frac_hbm_peak": round(r["rs_gbps"] / HBM_PEAK_GBPS, 4),
+                           "replaces_us_per_layer": round(r["torch_rope_us"] + r["sc_us"], 3),
+                           "replaces": "torch eager M-RoPE of q and k + store_kvcache scatter"},
             "scatter": {"us_per_layer": round(r["sc_us"], 3), "bytes": r["sc_bytes"],
-                        "gbps": round(r["sc_gbps"], 1), "frac_hbm_peak": round(r["sc_gbps"] / HBM_PEAK_GBPS, 4)},
+                        "gbps": round(r["sc_gbps"], 1), "frac_hbm_peak": round(r["sc_gbps"] / HBM_PEAK_GBPS, 4),
+                        "timing": "reference-API store_kvcache, timed outside the step"},
+            "torch_rope": {"us_per_layer": round(r["torch_rope_us"], 3)},
             "rerotate": None if r["rr_us"] is None else {
                 "us_all_layers": round(r["rr_us"], 2), "bytes": r["rr_bytes"], "gbps": round(r["rr_gbps"], 1),
                 "frac_hbm_peak": round(r["rr_gbps"] / HBM_PEAK_GBPS, 4),

@@ -58,6 +58,49 @@ int vlc_store_kvcache(const void* key, int64_t key_row_stride,
                       int64_t row_elems, int elem_bytes, void* stream);
 
 /*
+ * Rotary embedding of q and k fused with the paged KV store of k and v.
+ * Replaces RotaryEmbedding.forward (layers/rotary_embedding.py:37-48) followed
+ * by store_kvcache (layers/attention.py:33-40), the per-layer sequence at
+ * models/qwen3.py:84-85, with one launch.
+ *
+ * q: [num_tokens, num_heads_q, head_dim] bf16 at row stride q_row_stride; the
+ *   rotated q goes to q_out (row stride q_out_row_stride; q_out == q rotates in
+ *   place).  k: [num_tokens, num_heads_kv, head_dim] likewise; the rotated k goes
+ *   to row slot_mapping[n] of k_cache and, when k_out != NULL, to k_out.
+ *   v: rows copied bit for bit to row slot_mapping[n] of v_cache.  Heads are
+ *   contiguous rows of head_dim elements inside a token row; every pointer and
+ *   row stride must give 16-byte aligned rows.
+ * Pair i is dims (i, i + head_dim/2) (rotate-half).  Its angle comes from the
+ *   caller's fp32 cache cos_sin_cache[max_positions][cache_row_stride], whose
+ *   row p holds cos of pair i at column i and sin at column head_dim/2 + i (the
+ *   reference's cos_sin_cache, layers/rotary_embedding.py:30-35), at position
+ *   positions[section(i) * position_row_stride + n] (int64).
+ *   num_position_rows = 1: 1-D positions, section(i) = 0 for every pair.
+ *   num_position_rows = 3: M-RoPE rows (t, h, w); mrope_section is a HOST
+ *   int32[3] summing to head_dim/2: section(i) = 0 for i < s0, 1 for i < s0+s1,
+ *   else 2.
+ *   A position outside [0, max_positions) is clamped to the nearest valid row
+ *   (the reference's cache indexing raises instead).
+ * Arithmetic: y1 = x1*c - x2*s, y2 = x2*c + x1*s in fp32, each product and sum
+ *   rounded, then rounded to bf16 (nearest even): bit-identical to the
+ *   reference's fp32 formula (layers/rotary_embedding.py:6-14).
+ * k_cache/v_cache: rows of num_heads_kv*head_dim elements, num_slots rows each;
+ *   both NULL = rotate only (no store; v and slot_mapping may be NULL).  A slot
+ *   < 0 (the reference's -1) or >= num_slots is skipped.
+ * q_out must not overlap k, v or the caches; k_out must not overlap q or v.
+ */
+int vlc_rope_store_kvcache(const void* q, int64_t q_row_stride, void* q_out, int64_t q_out_row_stride,
+                           const void* k, int64_t k_row_stride, void* k_out, int64_t k_out_row_stride,
+                           const void* v, int64_t v_row_stride,
+                           int num_heads_q, int num_heads_kv, int head_dim,
+                           const int64_t* positions, int num_position_rows,
+                           int64_t position_row_stride, const int32_t* mrope_section,
+                           const float* cos_sin_cache, int64_t cache_row_stride,
+                           int64_t max_positions,
+                           void* k_cache, void* v_cache, int64_t num_slots,
+                           const int32_t* slot_mapping, int64_t num_tokens, void* stream);
+
+/*
  * All-layer copy of reused image KV with M-RoPE re-rotation of K.
  * Replaces ModelRunner.copy_image_kv (engine/model_runner.py:170-180), which
  * copies flat[:, :, new_slots] = flat[:, :, old_slots] on the cache viewed as

@@ -136,3 +136,56 @@ def mrope_positions(segments, spatial_merge_size: int = 2):
             parts.append(vision_position_ids(cur, val, spatial_merge_size))
             cur += max(int(val[1]), int(val[2])) // spatial_merge_size
     return np.concatenate(parts, axis=1).astype(np.int64), starts
+
+
+def rope_cache(max_positions: int, head_dim: int, theta: float) -> torch.Tensor:
+    """fp32 [max_positions, 1, head_dim] = cat(cos, sin) of t * inv_freq.
+
+    Restates RotaryEmbedding.__init__ (layers/rotary_embedding.py:29-35): the
+    angle of pair i at position t is the single fp32 product t * inv_freq[i].
+    """
+    t = torch.arange(max_positions, dtype=torch.float)
+    freqs = t[:, None] * inv_freq(head_dim, theta)[None, :]
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1)[:, None, :]
+
+
+def rope_rows(positions, cache: torch.Tensor, mrope_section=None):
+    """(cos, sin) fp32 [n, 1, head_dim/2] of every token's pairs.
+
+    1-D positions [n]: row positions[n] of the cache for every pair (the
+    reference's gather, layers/rotary_embedding.py:45-47).  M-RoPE positions
+    [3, n]: pair i reads row positions[section(i), n].
+    """
+    rows = cache.reshape(cache.shape[0], -1)
+    half = rows.shape[1] // 2
+    p = torch.as_tensor(np.asarray(positions), dtype=torch.long)
+    if p.dim() == 1:
+        cs = rows[p]
+        return cs[:, None, :half], cs[:, None, half:]
+    sec = torch.as_tensor(section_of_pair(2 * half, mrope_section))
+    pair = torch.arange(half)
+    pp = p[sec]  # [half, n]: position feeding pair i
+    cos = rows[pp, pair[:, None]].t()
+    sin = rows[pp, half + pair[:, None]].t()
+    return cos[:, None, :], sin[:, None, :]
+
+
+def rope_store_kvcache(positions, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: torch.Tensor,
+                       mrope_section=None, k_cache: torch.Tensor | None = None,
+                       v_cache: torch.Tensor | None = None, slot_mapping=None):
+    """Rotated (q, k) and, in place, the paged store of the rotated k and of v.
+
+    The per-layer sequence of models/qwen3.py:84-85: RotaryEmbedding.forward
+    (layers/rotary_embedding.py:37-48) on q and k, then store_kvcache
+    (layers/attention.py:33-40) of k and v.  q/k/v are bf16 [n, H, hd]; caches
+    are bf16 tensors viewed as [num_slots, Hkv * hd]; slot -1 is skipped.
+    """
+    cos, sin = rope_rows(positions, cache, mrope_section)
+    q_rot = apply_rotary_emb(q, cos, sin)
+    k_rot = apply_rotary_emb(k, cos, sin)
+    if k_cache is not None:
+        from .scatter import store_kvcache
+        store_kvcache(k_rot.view(torch.int16).numpy(), v.contiguous().view(torch.int16).numpy(),
+                      k_cache.view(torch.int16).numpy(), v_cache.view(torch.int16).numpy(),
+                      np.asarray(slot_mapping))
+    return q_rot, k_rot

@@ -204,3 +204,85 @@ def test_generate_runs_prefill_and_decode(dev):
     assert [len(o["token_ids"]) for o in out] == [3, 3]
     assert all(o["ttft"] > 0 for o in out)
     assert len(eng.scheduler.block_manager.image_kv_cache) == 1
+
+
+def _rope_module():
+    from vlcache_amd.layers.rotary_embedding import get_rope
+
+    return get_rope(128, 128, 4096, 1e6, {"mrope_section": [16, 24, 24]})
+
+
+@pytest.mark.parametrize("mode", ["paged_prefill", "contiguous_prefill", "decode"])
+def test_attention_forward_rope_equals_rope_then_forward(dev, mode):
+    say(f"layer: Attention.forward_rope vs rotary_emb then forward, {mode}, bit for bit")
+    hq, hkv, page = 16, 2, 256
+    rope = _rope_module().to(dev)
+    g = gen(60)
+    kc = torch.randn(6, page, hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(6, page, hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    if mode == "decode":
+        lens = [10, 300, 257]
+        bt = torch.tensor([[0, -1], [1, 2], [3, 4]], dtype=torch.int32)
+        cu_q, cu_k = [0, 1, 2, 3], [0, 10, 310, 567]
+        n = 3
+        slots = [bt[i, (m - 1) // page].item() * page + (m - 1) % page for i, m in enumerate(lens)]
+        pos = torch.tensor([[m - 1 for m in lens]] * 3, dtype=torch.int64)
+        ctx = lambda: set_context(False, torch.tensor(cu_q, dtype=torch.int32, device=dev),
+                                  torch.tensor(cu_k, dtype=torch.int32, device=dev), 1, 300,
+                                  torch.tensor(slots, dtype=torch.int32, device=dev),
+                                  torch.tensor(lens, dtype=torch.int32, device=dev), bt.to(dev),
+                                  cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
+    else:
+        paged = mode == "paged_prefill"
+        bt = torch.tensor([[5, 2, 7, -1], [5, 2, 7, -1]], dtype=torch.int32)
+        cu_q, cu_k = ([0, 300, 340], [0, 300, 700]) if paged else ([0, 300, 340], [0, 300, 340])
+        n = 340
+        s = np.concatenate([np.arange(300), np.arange(660, 700)])
+        slots = [bt[0, x // page].item() * page + x % page for x in s]
+        pos = torch.from_numpy(np.stack([s, s // 3, s % 17]).astype(np.int64))
+        ctx = lambda: set_context(True, torch.tensor(cu_q, dtype=torch.int32, device=dev),
+                                  torch.tensor(cu_k, dtype=torch.int32, device=dev), 300, max(cu_k[1:]),
+                                  torch.tensor(slots, dtype=torch.int32, device=dev), None,
+                                  bt.to(dev) if paged else None)
+    qkv = randn_bf16((n, (hq + 2 * hkv) * 128), 61).to(dev)
+    pos = pos.to(dev)
+
+    def views(buf):
+        return (buf[:, :hq * 128].view(n, hq, 128), buf[:, hq * 128:(hq + hkv) * 128].view(n, hkv, 128),
+                buf[:, (hq + hkv) * 128:].view(n, hkv, 128))
+
+    outs, caches = [], []
+    for fused in (False, True):
+        attn = Attention(hq, 128, 128 ** -0.5, hkv)
+        attn.k_cache, attn.v_cache = kc.clone(), vc.clone()
+        buf = qkv.clone()
+        q, k, v = views(buf)
+        ctx()
+        if fused:
+            o = attn.forward_rope(pos, q, k, v, rope, q_inplace=True)
+        else:
+            qr, kr = rope(pos, q, k)
+            o = attn(qr, kr, v)
+        reset_context()
+        torch.cuda.synchronize()
+        outs.append(bits(o))
+        caches.append((bits(attn.k_cache), bits(attn.v_cache)))
+    assert np.array_equal(outs[0], outs[1]), "attention output"
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
+
+
+def test_warm_request_logits_fused_rope_equals_torch_rope(dev, monkeypatch):
+    say("engine: warm partial request, fused RoPE+store vs torch RoPE + store_kvcache, logits bit for bit")
+    from vlcache_amd.qwen_vl import DecoderAttention
+
+    grid = (1, 16, 20)
+    toks_a, mm = _request(24, grid, 7, seed=7)
+    toks_b, _ = _request(33, grid, 5, seed=8)
+    res = []
+    for fused in (False, True):
+        monkeypatch.setattr(DecoderAttention, "fused_rope", fused)
+        eng = _engine(0.1)
+        _, la = _prefill_logits(eng, toks_a, mm)
+        _, lb = _prefill_logits(eng, toks_b, mm)
+        res.append((la, lb))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])

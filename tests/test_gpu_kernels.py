@@ -167,6 +167,119 @@ def test_rerotate_segments_negative_and_sectioned_deltas(dev):
     assert (out[0].view(torch.int16) != ref[0].view(torch.int16)).sum().item() == 0
 
 
+# ----------------------------------------------------------------------------- fused RoPE + scatter
+def _recomputed_mrope_positions():
+    """M-RoPE positions of the 1247 recomputed tokens of the 4K-image request (ratio 0.1)."""
+    pos, _ = orope.mrope_positions([("text", 128), ("image", (1, 154, 274)), ("text", 64)])
+    R = opre.recompute_count(0.1, 10549)
+    cols = np.concatenate([np.arange(0, 128 + R), np.arange(128 + 10549, 128 + 10549 + 64)])
+    return np.ascontiguousarray(pos[:, cols])
+
+
+def _rope_case(dev, positions, hq, hkv, section, seed, nb=8, bs=256, neg_every=5, store=True,
+               in_place=False, want_k=False, max_pos=16384, cache_offset=0, clamp_to=None):
+    """Fused kernel vs oracle (RotaryEmbedding then store_kvcache), all outputs bit for bit."""
+    hd = 128
+    positions = np.asarray(positions, dtype=np.int64)
+    n = positions.shape[-1]
+    g = gen(seed)
+    qkv = torch.randn(n, (hq + 2 * hkv) * hd, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * hd].view(n, hq, hd)
+    k = qkv[:, hq * hd:(hq + hkv) * hd].view(n, hkv, hd)
+    v = qkv[:, (hq + hkv) * hd:].view(n, hkv, hd)
+    cache = orope.rope_cache(max_pos, hd, 1e6)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(torch.int32)
+    if neg_every:
+        slots[::neg_every] = -1
+    kc = torch.randn(nb, bs, hkv, hd, generator=g).to(torch.bfloat16)  # canary contents
+    vc = torch.randn(nb, bs, hkv, hd, generator=g).to(torch.bfloat16)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    pos_ref = positions if clamp_to is None else np.clip(positions, 0, clamp_to - 1)
+    q_ref, k_ref = orope.rope_store_kvcache(pos_ref, q, k, v, cache, section,
+                                            kc_ref if store else None, vc_ref if store else None, slots.numpy())
+    qkv_d = qkv.to(dev)
+    q_d = qkv_d[:, :hq * hd].view(n, hq, hd)
+    k_d = qkv_d[:, hq * hd:(hq + hkv) * hd].view(n, hkv, hd)
+    v_d = qkv_d[:, (hq + hkv) * hd:].view(n, hkv, hd)
+    if cache_offset:  # rows at an address that is not 16-byte aligned: per-pair loads
+        buf = torch.zeros(cache.numel() + cache_offset, dtype=torch.float32, device=dev)
+        cache_d = buf[cache_offset:].view(cache.shape)
+        cache_d.copy_(cache.to(dev))
+    else:
+        cache_d = cache.to(dev)
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    q_out, k_out = kernels.rope_store_kvcache(
+        torch.from_numpy(positions).to(dev), q_d, k_d, v_d, cache_d, section,
+        kc_d if store else None, vc_d if store else None, slots.to(dev) if store else None,
+        q_out=q_d if in_place else None, return_k=want_k)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(q_out), bits(q_ref)), "rotated q"
+    if in_place:
+        assert np.array_equal(bits(qkv_d[:, :hq * hd]), bits(q_ref.reshape(n, -1)))
+    # k and v inputs are read only
+    assert np.array_equal(bits(qkv_d[:, hq * hd:]), bits(qkv[:, hq * hd:]))
+    if want_k:
+        assert np.array_equal(bits(k_out), bits(k_ref)), "rotated k (k_out)"
+    else:
+        assert k_out is None
+    if store:
+        assert np.array_equal(bits(kc_d), bits(kc_ref)), "k_cache"
+        assert np.array_equal(bits(vc_d), bits(vc_ref)), "v_cache"
+
+
+def test_rope_store_4k_image_recomputed_mrope(dev):
+    say("rope_store: 1247 recomputed tokens of the 4K-image request, M-RoPE [16,24,24], 16/2 heads, q in place")
+    pos = _recomputed_mrope_positions()
+    assert pos.shape == (3, 1247)
+    _rope_case(dev, pos, 16, 2, [16, 24, 24], seed=40, nb=84, in_place=True, neg_every=0)
+
+
+def test_rope_store_1d_7b_heads_k_out_and_skips(dev):
+    say("rope_store: 1-D positions, 28/4 heads, slot -1 every 5th, k_out, separate q_out")
+    _rope_case(dev, np.arange(300, 300 + 700), 28, 4, None, seed=41, nb=4, want_k=True)
+
+
+def test_rope_store_unaligned_sections_and_cache(dev):
+    say("rope_store: sections [10,27,27] and unaligned cache rows (per-pair path), distinct t/h/w")
+    g = np.random.default_rng(42)
+    pos = g.integers(0, 4000, size=(3, 333))
+    _rope_case(dev, pos, 16, 2, [10, 27, 27], seed=42, nb=2, cache_offset=1, max_pos=4096)
+    _rope_case(dev, pos, 16, 2, [16, 24, 24], seed=43, nb=2, cache_offset=1, max_pos=4096)
+
+
+def test_rope_store_rotate_only_and_clamped_positions(dev):
+    say("rope_store: no cache (rotation only) with k_out; positions outside the cache are clamped")
+    pos = np.array([0, 5, -3, 4095, 4096, 1 << 40, 17], dtype=np.int64)
+    _rope_case(dev, pos, 16, 2, None, seed=44, store=False, want_k=True, max_pos=4096, clamp_to=4096)
+    pos3 = np.stack([pos, pos[::-1].copy(), pos])
+    _rope_case(dev, pos3, 16, 2, [16, 24, 24], seed=45, nb=1, max_pos=4096, clamp_to=4096)
+
+
+def test_rope_store_out_of_range_slot_skipped(dev):
+    say("rope_store: slots beyond the cache are skipped, not written")
+    hq, hkv, hd, n = 4, 2, 128, 6
+    q = randn_bf16((n, hq, hd), 46)
+    k = randn_bf16((n, hkv, hd), 47)
+    v = randn_bf16((n, hkv, hd), 48)
+    cache = orope.rope_cache(64, hd, 1e6)
+    pos = np.arange(n)
+    slots = torch.tensor([0, 16, 3, 1 << 30, -1, 5], dtype=torch.int32)
+    kc = torch.zeros(1, 16, hkv, hd, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    keep = torch.tensor([0 <= s < 16 for s in slots.tolist()])
+    _, k_ref = orope.rope_store_kvcache(pos, q, k, v, cache)
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    kernels.rope_store_kvcache(torch.from_numpy(pos).to(dev), q.to(dev), k.to(dev), v.to(dev), cache.to(dev),
+                               None, kc_d, vc_d, slots.to(dev))
+    torch.cuda.synchronize()
+    kr, vr = kc.view(16, hkv, hd).clone(), vc.view(16, hkv, hd).clone()
+    idx = slots[keep].long()
+    kr[idx] = k_ref[keep]
+    vr[idx] = v[keep]
+    assert np.array_equal(bits(kc_d.view(16, hkv, hd)), bits(kr))
+    assert np.array_equal(bits(vc_d.view(16, hkv, hd)), bits(vr))
+
+
 # ----------------------------------------------------------------------------- attention
 def _paged_case(seed, hq, hkv, subseqs, page=256, extra_blocks=3, causal=True, shuffle=True):
     """Random q and a paged cache holding each virtual sequence's keys."""

@@ -158,3 +158,87 @@ def test_mrope_positions_4k_image_known_answer():
     assert img[1].min() == 128 and img[1].max() == 204
     assert img[2].min() == 128 and img[2].max() == 264
     assert list(pos[0, -64:]) == list(range(265, 329))
+
+
+# ----------------------------------------------------------------------------- fused RoPE + store oracle
+def test_rope_cache_matches_transformers_cos_sin():
+    """Row p of the cos/sin cache equals transformers' cos/sin at position p (first half of its 128 channels)."""
+    cache = orope.rope_cache(3000, 128, 1e6)[:, 0]
+    pos = np.arange(0, 3000, 7)
+    cos, sin = _hf_rotary()(torch.zeros(1, 1, 128), torch.as_tensor(np.stack([pos] * 3))[:, None, :])
+    assert torch.equal(cache[pos, :64], cos[0, 0, :, :64].float())
+    assert torch.equal(cache[pos, 64:], sin[0, 0, :, :64].float())
+    assert torch.equal(cos[0, 0, :, :64], cos[0, 0, :, 64:])  # transformers duplicates the half
+
+
+def test_rope_store_matches_transformers_mrope():
+    """fp32 q/k rotated by the oracle at M-RoPE positions == transformers' apply_multimodal_rotary_pos_emb."""
+    pos, _ = orope.mrope_positions([("text", 7), ("image", (1, 10, 14)), ("text", 9)])
+    n = pos.shape[1]
+    g = torch.Generator().manual_seed(30)
+    q = torch.randn(n, 4, 128, generator=g)
+    k = torch.randn(n, 2, 128, generator=g)
+    cache = orope.rope_cache(512, 128, 1e6)
+    q_rot, k_rot = orope.rope_store_kvcache(pos, q, k, None, cache, SECTION)
+    assert (q_rot - _hf_rotate(q, pos)).abs().max().item() < 1e-5
+    assert (k_rot - _hf_rotate(k, pos)).abs().max().item() < 1e-5
+
+
+def test_rope_store_planted_mistakes_are_caught():
+    """A wrong section order or a sign flip in the oracle breaks the transformers comparison."""
+    pos = np.stack([np.arange(40), 100 + np.arange(40), 300 + np.arange(40)])
+    k = torch.randn(40, 2, 128, generator=torch.Generator().manual_seed(31))
+    cache = orope.rope_cache(512, 128, 1e6)
+    ref = _hf_rotate(k, pos)
+    good, _ = orope.rope_store_kvcache(pos, k, k, None, cache, SECTION)
+    assert (good - ref).abs().max().item() < 1e-5
+    swapped, _ = orope.rope_store_kvcache(pos, k, k, None, cache, [24, 24, 16])
+    assert (swapped - ref).abs().max().item() > 1e-2
+    cos, sin = orope.rope_rows(pos, cache, SECTION)
+    flipped = orope.apply_rotary_emb(k, cos, -sin)
+    assert (flipped - ref).abs().max().item() > 1e-2
+
+
+def test_rope_store_1d_is_uniform_mrope_and_reference_gather():
+    """1-D positions == [3, n] with equal rows; both equal the reference's cache gather + chunk."""
+    g = torch.Generator().manual_seed(32)
+    q = torch.randn(50, 4, 128, generator=g).to(torch.bfloat16)
+    pos = np.random.default_rng(32).integers(0, 1000, 50)
+    cache = orope.rope_cache(1000, 128, 1e6)
+    a, _ = orope.rope_store_kvcache(pos, q, q, None, cache)
+    b, _ = orope.rope_store_kvcache(np.stack([pos] * 3), q, q, None, cache, SECTION)
+    cos, sin = cache[torch.as_tensor(pos)].chunk(2, dim=-1)  # layers/rotary_embedding.py:45-47
+    x1, x2 = torch.chunk(q.float(), 2, dim=-1)
+    c = torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(torch.bfloat16)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+
+
+def test_rope_store_scatter_semantics():
+    """Stored rows are the rotated k and the raw v; slot -1 and other rows untouched."""
+    g = torch.Generator().manual_seed(33)
+    n, hkv = 6, 2
+    q = torch.randn(n, 4, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(n, hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, hkv, 128, generator=g).to(torch.bfloat16)
+    kc = torch.randn(2, 8, hkv, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(2, 8, hkv, 128, generator=g).to(torch.bfloat16)
+    kc0, vc0 = kc.clone(), vc.clone()
+    slots = np.array([3, -1, 0, 15, 8, 9], dtype=np.int32)
+    cache = orope.rope_cache(64, 128, 1e6)
+    _, k_rot = orope.rope_store_kvcache(np.arange(n) + 5, q, k, v, cache, None, kc, vc, slots)
+    fk, fv, fk0, fv0 = kc.view(16, hkv, 128), vc.view(16, hkv, 128), kc0.view(16, hkv, 128), vc0.view(16, hkv, 128)
+    for i, s in enumerate(slots):
+        if s >= 0:
+            assert torch.equal(fk[s].view(torch.int16), k_rot[i].view(torch.int16))
+            assert torch.equal(fv[s].view(torch.int16), v[i].view(torch.int16))
+    untouched = [r for r in range(16) if r not in set(slots.tolist())]
+    assert torch.equal(fk[untouched], fk0[untouched]) and torch.equal(fv[untouched], fv0[untouched])
+    assert not torch.equal(k_rot, k)  # positions 5.. rotate
+
+
+def test_rope_cache_matches_engine_rotary_module():
+    from vlcache_amd.layers.rotary_embedding import MRotaryEmbedding
+
+    m = MRotaryEmbedding(128, 128, 2048, 1e6, SECTION)
+    assert torch.equal(m.cos_sin_cache, orope.rope_cache(2048, 128, 1e6))

@@ -28,6 +28,11 @@ SIGNATURES = {
     "vlc_abi_version": (i32, []),
     "vlc_status_string": (ctypes.c_char_p, [i32]),
     "vlc_store_kvcache": (i32, [vp, i64, vp, i64, vp, vp, i64, vp, i64, i64, i32, vp]),
+    "vlc_rope_store_kvcache": (
+        i32,
+        [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp, i32, i64, c_i32p, vp, i64,
+         i64, vp, vp, i64, vp, i64, vp],
+    ),
     "vlc_rerotate_copy_kv": (
         i32,
         [vp, i64, i64, i32, vp, vp, i64, i64, i32, i32, vp, vp, i32, i32, vp],

@@ -48,8 +48,18 @@ class ModelRunner:
         self.device = torch.device("cuda", 0)
         torch.cuda.set_device(self.device)
         self.dtype = hf.torch_dtype
-        with torch.device(self.device):
-            self.model = Qwen2_5_VLForConditionalGeneration(hf).to(self.dtype)
+        # Built under the default dtype, as the reference does (engine/model_runner.py:33-34):
+        # parameters are bf16 while tensors created with an explicit dtype, such as the
+        # fp32 rotary cos/sin cache, keep it.  A blanket .to(bf16) would round that cache.
+        prev = torch.get_default_dtype()
+        torch.set_default_dtype(self.dtype)
+        try:
+            with torch.device(self.device):
+                self.model = Qwen2_5_VLForConditionalGeneration(hf)
+        finally:
+            torch.set_default_dtype(prev)
+        assert all(m.cos_sin_cache.dtype == torch.float32 for m in self.model.modules()
+                   if hasattr(m, "cos_sin_cache"))
         random_init_(self.model, seed=config.seed)
         self.model.eval()
         self.sampler = Sampler()

@@ -4,11 +4,13 @@ One warm request (or a batch of them) runs, per step:
   1. the all-layer reuse copy of the cached image KV with K re-rotated to the
      image's new position (one launch; ModelRunner.copy_image_kv,
      engine/model_runner.py:170-180);
-  2. per layer, the scatter of the recomputed tokens' K/V into the paged cache
-     (store_kvcache, layers/attention.py:62-63) and the varlen paged GQA causal
-     attention of the recomputed queries against the whole cache
-     (layers/attention.py:64-70).
-Inputs are seeded N(0, 1) bf16: cached K/V, the recomputed tokens' q/k/v.
+  2. per layer, the rotary embedding of the recomputed tokens' q and k at their
+     M-RoPE positions fused with the store of k and v into the paged cache
+     (RotaryEmbedding.forward + store_kvcache, layers/rotary_embedding.py:37-48,
+     layers/attention.py:62-63), then the varlen paged GQA causal attention of
+     the recomputed queries against the whole cache (layers/attention.py:64-70).
+Inputs are seeded N(0, 1) bf16: cached K/V, the recomputed tokens' q/k/v rows
+as the QKV projection lays them out (q, k and v are views of one buffer).
 Block ids are a seeded permutation of the pool; the cached image's blocks and
 each request's blocks are disjoint, as the reference's allocator guarantees
 (the cached entry's blocks stay referenced, engine/block_manager.py:91-94).
@@ -19,7 +21,11 @@ import numpy as np
 import torch
 
 from . import kernels
-from .workloads import BLOCK_SIZE, Workload
+from .engine.positions import mrope_positions
+from .layers.rotary_embedding import get_rope
+from .workloads import BLOCK_SIZE, IMAGE_TOKEN_ID, Workload
+
+MAX_POSITIONS = 128000  # Qwen2.5-VL max_position_embeddings: rows of the rotary cache
 
 
 def _slots(bt, positions):
@@ -63,7 +69,7 @@ class WarmPrefillHotPath:
 
         # reuse copy: old -> new slots per request, one rotation segment per request
         old, new, seg, deltas = [], [], [], []
-        slot_map, bts, cu_q, cu_k = [], [], [0], [0]
+        slot_map, bts, cu_q, cu_k, pos_cols = [], [], [0], [0], []
         for i, (r, bt) in enumerate(zip(reqs, seq_bts)):
             img_s, img_e = r.prefix, r.prefix + r.n_image
             reuse = np.arange(img_s + r.R, img_e) if r.ratio > 0 else np.arange(0)
@@ -76,6 +82,10 @@ class WarmPrefillHotPath:
             else:
                 comp = np.arange(r.length)
             slot_map.append(_slots(bt, comp))
+            toks = np.ones(r.length, dtype=np.int64)
+            toks[img_s:img_e] = IMAGE_TOKEN_ID
+            pos_all, _, _ = mrope_positions(toks, [(1, 2 * r.grid_hw[0], 2 * r.grid_hw[1])], IMAGE_TOKEN_ID)
+            pos_cols.append(pos_all[:, comp])
             row = np.full(max(seq_nbs), -1, dtype=np.int32)
             row[:len(bt)] = bt
             for sq, sk in r.subseqs():
@@ -96,13 +106,22 @@ class WarmPrefillHotPath:
         self.cu_k = torch.tensor(cu_k, dtype=torch.int32, device=dev)
         self.slot_mapping = torch.from_numpy(np.concatenate(slot_map).astype(np.int32)).to(dev)
         self.block_tables = torch.from_numpy(np.stack(bts)).to(dev)
-        # recomputed tokens: qkv rows as the QKV projection lays them out; k is a
-        # separate contiguous tensor (it comes out of RoPE), v a strided view
+        # recomputed tokens: qkv rows as the QKV projection lays them out (q, k and
+        # v are strided views); rope_store writes the rotated q to a contiguous
+        # tensor, as RotaryEmbedding returns one, and leaves the inputs unchanged.
         qkv = torch.randn(n_q, (hq + 2 * hkv) * hd, generator=g, device=dev, dtype=torch.bfloat16)
-        self.q = qkv[:, :hq * hd].reshape(n_q, hq, hd).contiguous()
-        self.k = qkv[:, hq * hd:(hq + hkv) * hd].reshape(n_q, hkv, hd).contiguous()
-        self.v = qkv[:, (hq + hkv) * hd:].view(n_q, hkv, hd)
         self.qkv = qkv
+        self.q_in = qkv[:, :hq * hd].view(n_q, hq, hd)
+        self.k_in = qkv[:, hq * hd:(hq + hkv) * hd].view(n_q, hkv, hd)
+        self.v = qkv[:, (hq + hkv) * hd:].view(n_q, hkv, hd)
+        self.q = torch.empty(n_q, hq, hd, device=dev, dtype=torch.bfloat16)   # rotated q
+        self.k = torch.empty(n_q, hkv, hd, device=dev, dtype=torch.bfloat16)  # rotated k (contiguous)
+        self.positions = torch.from_numpy(np.ascontiguousarray(np.concatenate(pos_cols, axis=1))).to(dev)
+        self.rope = get_rope(hd, hd, MAX_POSITIONS, m.rope_theta, {"mrope_section": list(m.mrope_section)}).to(dev)
+        self.rope_k_out = not any(r.ratio > 0 for r in reqs)  # contiguous attention reads the fresh keys
+        # rotated q and k (no store) so that attention and scatter have valid inputs before a step
+        kernels.rope_store_kvcache(self.positions, self.q_in, self.k_in, self.v, self.rope.cos_sin_cache,
+                                   m.mrope_section, q_out=self.q, k_out=self.k)
         self.scale = hd ** -0.5
         # Block tables exist only when a request is partial; otherwise attention
         # reads the fresh contiguous k/v (engine/model_runner.py:294-299,
@@ -111,12 +130,24 @@ class WarmPrefillHotPath:
         self.plan = kernels.plan_attention(cu_q, cu_k, hq, hkv, hd, True, dev)
         self.out = torch.empty(n_q, hq, hd, dtype=torch.bfloat16, device=dev)
 
-    # ---- the three kernels ----
+    # ---- the kernels ----
     def rerotate(self):
         kernels.rerotate_copy_kv(self.kv_cache, self.old_slots, self.new_slots, self.cos_sin, self.seg,
                                  rotate_k=self.rotate)
 
+    def rope_store(self, layer: int):
+        """Rotate q and k at the M-RoPE positions; store rotated k and v in layer's cache."""
+        kernels.rope_store_kvcache(self.positions, self.q_in, self.k_in, self.v, self.rope.cos_sin_cache,
+                                   self.model.mrope_section, self.k_caches[layer], self.v_caches[layer],
+                                   self.slot_mapping, q_out=self.q,
+                                   k_out=self.k if self.rope_k_out else None)
+
+    def torch_rope(self):
+        """The unfused reference sequence's rotation: torch eager RoPE of q and k."""
+        return self.rope(self.positions, self.q_in, self.k_in)
+
     def scatter(self, layer: int):
+        """store_kvcache of the rotated k and of v (the reference's separate scatter)."""
         kernels.store_kvcache_raw(self.k, self.v, self.k_caches[layer], self.v_caches[layer],
                                   self.slot_mapping)
 
@@ -132,6 +163,6 @@ class WarmPrefillHotPath:
         if self.n_reused:
             self.rerotate()
         for layer in range(self.model.num_layers):
-            self.scatter(layer)
+            self.rope_store(layer)
             self.attention(layer)
         return self.out

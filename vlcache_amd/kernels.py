@@ -65,6 +65,94 @@ def store_kvcache_raw(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     _lib.check("vlc_store_kvcache", st)
 
 
+# --------------------------------------------------------------------------- fused RoPE + scatter
+def _check_heads(name: str, t: torch.Tensor, n: int, heads: int, hd: int) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bf16")
+    if t.dim() != 3 or tuple(t.shape) != (n, heads, hd):
+        raise ValueError(f"{name}: expected [{n}, {heads}, {hd}], got {tuple(t.shape)}")
+    if t.stride(-1) != 1 or t.stride(1) != hd:
+        raise ValueError(f"{name}: heads must be contiguous rows of {hd} elements")
+
+
+def rope_store_kvcache(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
+                       cos_sin_cache: torch.Tensor, mrope_section=None,
+                       k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
+                       slot_mapping: torch.Tensor | None = None, q_out: torch.Tensor | None = None,
+                       k_out: torch.Tensor | None = None, return_k: bool = False):
+    """Rotate q and k and store the rotated k and v into the paged cache (vlc_rope_store_kvcache).
+
+    One launch for RotaryEmbedding.forward (layers/rotary_embedding.py:37-48) plus
+    store_kvcache (layers/attention.py:33-40).  positions: int64 [N] (1-D) or
+    [3, N] (M-RoPE, with mrope_section); q [N, Hq, hd], k/v [N, Hkv, hd] bf16
+    with contiguous head rows (any token row stride, e.g. views of the QKV
+    output); cos_sin_cache: the rotary module's fp32 [max_pos, (1,) hd] cache.
+    Caches and slot_mapping may be None (rotation only).  Returns (q_rot, k_rot):
+    q_rot is q_out (a new contiguous tensor when None; pass q_out=q to rotate in
+    place); k_rot is k_out, a new tensor when return_k, else None.
+    """
+    _require_device("rope_store_kvcache", positions, q, k, v, cos_sin_cache, k_cache, v_cache, slot_mapping,
+                    q_out, k_out)
+    n, hq, hd = q.shape
+    hkv = k.shape[1]
+    _check_heads("q", q, n, hq, hd)
+    _check_heads("k", k, n, hkv, hd)
+    if positions.dtype != torch.int64 or positions.stride(-1) != 1:
+        raise TypeError("positions must be int64 with contiguous rows")
+    if positions.dim() == 1:
+        rows, pos_rs, sec = 1, 0, None
+        if positions.numel() != n:
+            raise ValueError("positions must hold one entry per token")
+    elif positions.dim() == 2 and positions.shape[0] == 3:
+        if mrope_section is None:
+            raise ValueError("[3, N] positions need mrope_section")
+        if positions.shape[1] != n:
+            raise ValueError("positions must hold one column per token")
+        rows, pos_rs = 3, positions.stride(0)
+        sec = (ctypes.c_int32 * 3)(*[int(x) for x in mrope_section])
+    else:
+        raise ValueError("positions must be [N] or [3, N]")
+    cs = cos_sin_cache
+    if cs.dtype != torch.float32 or cs.shape[-1] != hd or cs.stride(-1) != 1:
+        raise ValueError(f"cos_sin_cache must be fp32 [max_pos, (1,) {hd}] with contiguous rows")
+    if cs.dim() == 3 and cs.shape[1] != 1 or cs.dim() not in (2, 3):
+        raise ValueError("cos_sin_cache must be [max_pos, hd] or [max_pos, 1, hd]")
+    store = k_cache is not None or v_cache is not None
+    num_slots = 0
+    if store:
+        if k_cache is None or v_cache is None or slot_mapping is None or v is None:
+            raise ValueError("storing needs k_cache, v_cache, slot_mapping and v")
+        _check_heads("v", v, n, hkv, hd)
+        if slot_mapping.dtype != torch.int32 or slot_mapping.numel() != n:
+            raise ValueError("slot_mapping must be int32 [N]")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("k_cache/v_cache must be contiguous")
+        if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+            raise TypeError("caches must be bf16")
+        num_slots = k_cache.numel() // (hkv * hd)
+        if v_cache.numel() // (hkv * hd) != num_slots or k_cache.shape[-1] != hd or k_cache.shape[-2] != hkv:
+            raise ValueError("caches must be [..., Hkv, hd] of equal size")
+    if q_out is None:
+        q_out = torch.empty(n, hq, hd, dtype=torch.bfloat16, device=q.device)
+    else:
+        _check_heads("q_out", q_out, n, hq, hd)
+    if k_out is None and return_k:
+        k_out = torch.empty(n, hkv, hd, dtype=torch.bfloat16, device=q.device)
+    elif k_out is not None:
+        _check_heads("k_out", k_out, n, hkv, hd)
+    st = _lib.load().vlc_rope_store_kvcache(
+        q.data_ptr(), q.stride(0), q_out.data_ptr(), q_out.stride(0),
+        k.data_ptr(), k.stride(0), k_out.data_ptr() if k_out is not None else None,
+        k_out.stride(0) if k_out is not None else 0,
+        v.data_ptr() if v is not None else None, v.stride(0) if v is not None else 0,
+        hq, hkv, hd, positions.data_ptr(), rows, pos_rs, sec,
+        cs.data_ptr(), cs.stride(0), cs.shape[0],
+        k_cache.data_ptr() if store else None, v_cache.data_ptr() if store else None, num_slots,
+        slot_mapping.data_ptr() if store else None, n, _stream(q))
+    _lib.check("vlc_rope_store_kvcache", st)
+    return q_out, k_out
+
+
 # --------------------------------------------------------------------------- rerotate
 def rerotation_table(deltas, head_dim: int, theta: float, mrope_section=None,
                      device=None) -> torch.Tensor:

@@ -9,7 +9,9 @@ Same public surface as layers/attention.py of the reference:
     one (the cache is read back after the scatter, :65-66) and over the fresh
     contiguous k/v otherwise; decode attends through the block table with one
     query per sequence and returns [B, 1, Hq, hd] (:71-74).
-Both attention forms run in the gfx950 varlen GQA kernel.
+Both attention forms run in the gfx950 varlen GQA kernel.  forward_rope(positions,
+q, k, v, rotary_emb) is the fused form of the caller's sequence RoPE -> forward
+(models/qwen3.py:84-85): one kernel rotates q and k and stores k and v.
 """
 from __future__ import annotations
 
@@ -57,6 +59,32 @@ class Attention(nn.Module):
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and v_cache.numel():
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+        return self._attend(q, k, v, context)
+
+    def forward_rope(self, positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     rotary_emb, q_inplace: bool = False) -> torch.Tensor:
+        """rotary_emb(positions, q, k) then forward(q, k, v) (models/qwen3.py:84-85), bit for bit,
+        with the rotation and the KV store in one kernel (kernels.rope_store_kvcache).
+
+        rotary_emb is the layer's RotaryEmbedding / MRotaryEmbedding: its fp32
+        cos/sin cache and, for [3, N] positions, its mrope_section.  q_inplace
+        rotates q inside the caller's buffer (e.g. the QKV projection output)
+        instead of a new tensor.
+        """
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        store = bool(k_cache.numel() and v_cache.numel())
+        # Without a block table the prefill attends over the fresh keys, so it needs them rotated.
+        need_k = context.is_prefill and (context.block_tables is None or not store)
+        section = getattr(rotary_emb, "mrope_section", None) if positions.dim() == 2 else None
+        q, k_rot = kernels.rope_store_kvcache(
+            positions, q, k, v, rotary_emb.cos_sin_cache, section,
+            k_cache if store else None, v_cache if store else None,
+            context.slot_mapping if store else None, q_out=q if q_inplace else None, return_k=need_k)
+        return self._attend(q, k_rot, v, context)
+
+    def _attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, context: Context) -> torch.Tensor:
+        k_cache, v_cache = self.k_cache, self.v_cache
         if context.is_prefill:
             if context.block_tables is not None:
                 k, v = k_cache, v_cache

@@ -6,8 +6,9 @@ Qwen2.5-VL variant: QKV bias, no q/k norm) and of
 Qwen2_5_VLForConditionalGeneration.forward (models/qwen2_5_vl.py:562-580: the
 image-token rows of the embeddings are replaced by visual embeddings).
 
-GEMMs, norms and the MLP stay on torch (hipBLASLt) and run eagerly; the
-attention of every layer is the gfx950 kernel via layers.attention.Attention.
+GEMMs, norms and the MLP stay on torch (hipBLASLt) and run eagerly; per layer
+the rotary embedding of q and k and the KV store run as one gfx950 kernel and
+the attention as another, via layers.attention.Attention.
 The vision tower is not part of this path: visual embeddings come from the
 encoder cache (warm request) or are supplied by the caller.
 Weights are random N(0, 0.02) unless loaded by the caller.
@@ -45,6 +46,10 @@ class RMSNorm(nn.Module):
 
 
 class DecoderAttention(nn.Module):
+    # True: RoPE and the KV store run as one kernel (Attention.forward_rope);
+    # False: the reference's sequence, torch RoPE then Attention.forward.
+    fused_rope = True
+
     def __init__(self, cfg):
         super().__init__()
         self.num_heads = cfg.num_attention_heads
@@ -64,8 +69,12 @@ class DecoderAttention(nn.Module):
         q = q.view(-1, self.num_heads, self.head_dim)
         k = k.view(-1, self.num_kv_heads, self.head_dim)
         v = v.view(-1, self.num_kv_heads, self.head_dim)  # strided view into qkv rows
-        q, k = self.rotary_emb(positions, q, k)
-        o = self.attn(q, k, v)
+        if self.fused_rope:
+            # one kernel: rotate q (in the qkv buffer) and k, store rotated k and v in the cache
+            o = self.attn.forward_rope(positions, q, k, v, self.rotary_emb, q_inplace=True)
+        else:
+            q, k = self.rotary_emb(positions, q, k)
+            o = self.attn(q, k, v)
         return self.o_proj(o.flatten(1, -1))
 
 

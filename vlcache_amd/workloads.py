@@ -151,3 +151,14 @@ def rerotate_bytes(n_tokens: int, num_layers: int, num_kv_heads: int, head_dim: 
 def scatter_bytes(n_tokens: int, num_kv_heads: int, head_dim: int) -> int:
     """HBM bytes of one layer's store_kvcache: K and V rows read and written (bf16)."""
     return 2 * n_tokens * num_kv_heads * head_dim * 2 * 2
+
+
+def rope_store_bytes(n_tokens: int, num_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    """HBM bytes of one layer's fused RoPE + KV store.
+
+    q rows read and written, k and v rows read and written to the cache (bf16),
+    plus per token its cos/sin row (head_dim fp32), three int64 positions and
+    the int32 slot.
+    """
+    rows = 2 * (num_heads + 2 * num_kv_heads) * head_dim * 2
+    return n_tokens * (rows + head_dim * 4 + 3 * 8 + 4)
