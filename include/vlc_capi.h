@@ -182,6 +182,56 @@ int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride,
                         void* out, int64_t out_row_stride,
                         void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Host-side sizing for vlc_decode_attn (no device calls).
+ * The reference's decode call, flash_attn_with_kvcache at layers/attention.py:71-74,
+ * sizes its split-KV work inside the external flash-attn library; here the caller
+ * asks once per step (or once per maximum context length) for:
+ *   *key_chunk      keys per workgroup (a multiple of 128),
+ *   *grid_splits    workgroups per (sequence, kv head) the launch provides, enough
+ *                   for max_seqlen_k keys,
+ *   *workspace_bytes  device workspace the call needs.
+ *   *pipeline_out   the kernel shape to launch with.
+ * num_splits > 0 forces the number of chunks for max_seqlen_k; 0 chooses one
+ * wave of workgroups over the compute units (num_cus, 0 selects 256), at most 32
+ * chunks per pair.  pipeline selects the kernel shape, 16 * waves per workgroup +
+ * stages per wave, one of 0x42, 0x22, 0x23, 0x24, 0x14; 0 chooses.
+ * Requires head_dim == 128, num_heads_q / num_heads_kv <= 16, page_size % 32 == 0.
+ */
+int vlc_decode_attn_plan(int batch, int num_heads_q, int num_heads_kv, int head_dim, int page_size,
+                         int max_seqlen_k, int num_cus, int num_splits, int pipeline,
+                         int32_t* key_chunk, int32_t* grid_splits, int32_t* pipeline_out,
+                         int64_t* workspace_bytes);
+
+/*
+ * Paged GQA decode attention: one query per sequence against its paged cache.
+ * Replaces flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ * cache_seqlens=context_lens, block_table=block_tables, softmax_scale, causal=True)
+ * at layers/attention.py:71-74.
+ *
+ * q: [batch, num_heads_q, head_dim] bf16, q_row_stride elements between sequences
+ *   (heads are contiguous rows of head_dim).  out: same shape, out_row_stride.
+ * k_cache/v_cache: [num_blocks, page_size, num_heads_kv, head_dim] bf16 with
+ *   cache_row_stride elements per token row.  Key j of sequence b is row
+ *   block_table[b*bt_row_stride + j/page_size]*page_size + j%page_size.
+ * cache_seqlens: DEVICE int32 [batch], keys per sequence; sequence b attends keys
+ *   [0, cache_seqlens[b]) (the query is the last position, so causal masking
+ *   hides nothing).  Lengths are clamped to bt_cols*page_size and to
+ *   grid_splits*key_chunk; a sequence with no key gets zeros; a block id outside
+ *   [0, num_blocks) reads as zeros.
+ * key_chunk, grid_splits, pipeline: from vlc_decode_attn_plan for an upper bound
+ *   of the lengths.  workspace: device memory of at least the planned bytes, whose first
+ *   batch*num_heads_kv 32-bit words must be zero before the first call; every
+ *   call leaves them zero.  Calls that share a workspace must not overlap.
+ */
+int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                    int64_t cache_row_stride, int page_size, int64_t num_blocks,
+                    const int32_t* block_table, int64_t bt_row_stride, int bt_cols,
+                    const int32_t* cache_seqlens, int batch, int num_heads_q, int num_heads_kv,
+                    int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
+                    void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -396,3 +396,70 @@ def test_attention_contiguous_dense_strided_v(dev):
     v = qkv[:, (hq + hkv) * 128:].reshape(n, hkv, 128)
     ref = oattn.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, True, None)
     assert_close(out.cpu(), ref, what="dense contiguous")
+
+
+# ----------------------------------------------------------------------------- decode attention
+def _decode_case(dev, lens, hq, hkv, seed, page=256, num_splits=0, extra_blocks=2, reps=1, pipeline=0):
+    """Paged decode (one query per sequence) vs the fp32 oracle; returns the outputs of every rep."""
+    g = gen(seed)
+    B = len(lens)
+    nbs = [max(1, -(-n // page)) for n in lens]
+    nb = sum(nbs) + extra_blocks
+    ids = torch.randperm(nb, generator=g).tolist()
+    bt = torch.full((B, max(nbs)), -1, dtype=torch.int32)
+    p = 0
+    for b, n in enumerate(nbs):
+        bt[b, :n] = torch.tensor(ids[p:p + n], dtype=torch.int32)
+        p += n
+    q = torch.randn(B, hq, 128, generator=g).to(torch.bfloat16)
+    kc = torch.randn(nb, page, hkv, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, page, hkv, 128, generator=g).to(torch.bfloat16)
+    cu_q = list(range(B + 1))
+    cu_k = [0]
+    for n in lens:
+        cu_k.append(cu_k[-1] + n)
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), page)
+    plan = kernels.plan_decode(B, hq, hkv, 128, page, max(lens), dev, num_splits=num_splits, pipeline=pipeline)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    sl, btd = torch.tensor(lens, dtype=torch.int32, device=dev), bt.to(dev)
+    outs = []
+    for _ in range(reps):
+        o = kernels.decode_attention(qd, kd, vd, sl, btd, 128 ** -0.5, plan=plan)
+        torch.cuda.synchronize()
+        outs.append(o.cpu())
+    for o in outs:
+        assert_close(o, ref, what=f"decode {lens} hq={hq} hkv={hkv} splits={num_splits}")
+    return outs, plan
+
+
+def test_decode_7b_batch4_13k_context(dev):
+    say("decode: 7B heads 28/4, batch 4, contexts 13432..13435, page 256")
+    _, plan = _decode_case(dev, [13432, 13433, 13434, 13435], 28, 4, seed=60)
+    assert plan.grid_splits > 1  # split-KV with the in-kernel merge
+
+
+def test_decode_3b_ragged_lengths_and_empty(dev):
+    say("decode: 3B heads 16/2, lengths 0, 1, 31, 32, 33, 700, 10741")
+    lens = [0, 1, 31, 32, 33, 700, 10741]
+    outs, _ = _decode_case(dev, lens, 16, 2, seed=61)
+    assert torch.count_nonzero(outs[0][0]) == 0  # no key: zeros
+
+
+@pytest.mark.parametrize("splits", [1, 3, 32])
+def test_decode_forced_splits_repeatable(dev, splits):
+    say(f"decode: forced {splits} chunks, 3 calls in a row (ticket counters reset), bit-identical")
+    outs, plan = _decode_case(dev, [5000, 777, 3001], 16, 2, seed=62, num_splits=splits, reps=3)
+    assert all(torch.equal(outs[0].view(torch.int16), o.view(torch.int16)) for o in outs[1:])
+    assert int(plan.workspace[:4 * 3 * 2].view(torch.int32).count_nonzero()) == 0  # counters back at zero
+
+
+@pytest.mark.parametrize("pipeline", [0x42, 0x22, 0x23, 0x24, 0x14])
+def test_decode_pipeline_shapes(dev, pipeline):
+    say(f"decode: kernel shape {pipeline:#x} (waves x stages), ragged lengths, 3 and 1 chunks")
+    _decode_case(dev, [1, 95, 2500, 6000], 28, 4, seed=64, pipeline=pipeline, num_splits=3)
+    _decode_case(dev, [33, 4000], 16, 2, seed=65, pipeline=pipeline, num_splits=1)
+
+
+def test_decode_small_pages_group7(dev):
+    say("decode: page 32, 7 q heads per kv head, lengths 95, 96, 97, 4000")
+    _decode_case(dev, [95, 96, 97, 4000], 28, 4, seed=63, page=32)

@@ -37,6 +37,12 @@ SIGNATURES = {
         i32,
         [vp, i64, i64, i32, vp, vp, i64, i64, i32, i32, vp, vp, i32, i32, vp],
     ),
+    "vlc_decode_attn_plan": (i32, [i32, i32, i32, i32, i32, i32, i32, i32, i32, c_i32p, c_i32p, c_i32p, c_i64p]),
+    "vlc_decode_attn": (
+        i32,
+        [vp, i64, vp, vp, i64, i32, i64, vp, i64, i32, vp, i32, i32, i32, i32, f32, i32, i32, i32, vp, i64,
+         vp, i64, vp],
+    ),
     "vlc_attn_plan": (
         i32,
         [c_i32p, c_i32p, i32, i32, i32, i32, i32, i32, c_i32p, i64, c_i64p, c_i64p],

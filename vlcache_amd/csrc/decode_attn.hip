@@ -1,0 +1,588 @@
+// Paged GQA decode attention for gfx950: the replacement of
+// flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache, cache_seqlens=context_lens,
+// block_table=block_tables, softmax_scale=scale, causal=True) at layers/attention.py:71-74.
+//
+// One query per sequence; query b attends keys [0, cache_seqlens[b]) of its paged
+// cache.  The work is bandwidth: every K/V row of every sequence is read once.
+//
+// Decomposition: one workgroup per (key chunk, kv head, sequence), grid
+// (splits, Hkv, B).  Its four waves each stream a contiguous quarter of the
+// chunk in 32-key tiles, double-buffered global -> LDS by DMA into the wave's own
+// LDS region, so the waves never wait for each other inside the loop.  The 16
+// MFMA columns are the q heads of the kv head (group <= 16):
+//   S^T (16 keys x 16 heads) = K (16 x 32 dims) . Q^T        v_mfma_f32_16x16x32_bf16
+//   O^T (16 dims x 16 heads) += V^T (16 dims x 32 keys) . P^T
+// A lane owns one head and 4 keys of each 16-key block, so P^T leaves the S^T
+// accumulators already in the B-operand layout of the second product; V is
+// read transposed from LDS (ds_read_b64_tr_b16).  The column max and sum cross
+// the four 16-lane groups with v_permlane16_swap / v_permlane32_swap (VALU).
+//
+// Merge: the four waves merge (O, m, l) through LDS.  A sequence-head pair whose
+// keys span several chunks writes each chunk's (O, m, l) to the workspace; the
+// workgroup that finishes last (a device-scope ticket counter, taken once the
+// partials have landed) merges all chunks with the log-sum-exp rule, writes the
+// output and resets its counter to zero, so one launch does the whole call.
+#include <algorithm>
+
+#include "common.h"
+
+namespace vlc {
+namespace decode {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kTileKeys = 32;                     // keys per wave tile
+constexpr int kCols = 16;                         // MFMA columns = q heads of one kv head
+constexpr int kTileBytes = kTileKeys * kHeadDim * 2;  // 8 KB of K (or V) per tile
+constexpr int kStageBytes = 2 * kTileBytes;       // one pipeline stage: K + V of a tile
+constexpr int kWgKeys = 4 * kTileKeys;            // key chunks are multiples of this (128)
+constexpr int kMaxPagesPerWave = 64;              // block ids a wave keeps in a register
+constexpr int kDmaPerTile = 16;                   // global_load_lds_dwordx4 per tile (8 K + 8 V)
+
+// Pipeline shapes (waves per workgroup W, stages per wave S): a wave keeps S - 1
+// tiles in flight while it computes one, in W * S * 16 KB of LDS.  S <= 4 keeps
+// the wait count 16 (S - 1) within vmcnt's range.
+constexpr int pipeline_code(int w, int s) { return 16 * w + s; }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct Params {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* block_table;
+  const int32_t* seqlens;
+  uint16_t* out;
+  uint32_t* counters;  // [B * Hkv], zero between calls
+  float* part_ml;      // [B * Hkv][grid_splits][kCols][2]: (m in scaled log2 units, l)
+  float* part_o;       // [B * Hkv][grid_splits][kCols][kHeadDim]: unnormalised O
+  int64_t q_row_stride;    // elements between sequences of q
+  int64_t out_row_stride;  // elements between sequences of out
+  int64_t cache_row_stride;  // elements per cache row (token)
+  int64_t bt_row_stride;
+  int64_t num_blocks;
+  int page_size;
+  int bt_cols;
+  int group;
+  int num_heads_kv;
+  int key_chunk;    // keys per workgroup (multiple of kWgKeys)
+  int max_keys;     // keys the grid and the block table cover
+  float scale_log2;
+};
+
+// All-zero row: the source of keys past the end of a sequence and of pages whose
+// block id is outside the cache.
+__device__ __attribute__((aligned(256))) const uint32_t kZeroRow[64] = {};
+
+// 16-byte chunk c of LDS row r lives in slot c ^ swizzle(r).
+//   K (read 16 rows x one chunk per 16-lane group, ds_read_b128): r mod 16.
+//   V (transpose reads: rows 4q + f, chunks 2mb, 2mb + 1 for groups q = 0, 1 of a
+//   half-wave): bits 2-3 follow r mod 4, bit 1 follows (r / 4) mod 2, so the 16
+//   (row, chunk) pairs of a half-wave hit 16 distinct slots.
+__device__ __forceinline__ int swz_k(int r) { return r & 15; }
+__device__ __forceinline__ int swz_v(int r) { return ((r & 3) << 2) | (((r >> 2) & 1) << 1); }
+
+__device__ __forceinline__ uint32_t lds_u32(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const lds_void*)ptr;
+}
+// global_load_lds_dwordx4 from a per-lane 64-bit address: lane i's 16 bytes land at
+// LDS M0 + 16 i.  Issued through inline assembly so that the compiler does not model
+// it as a flat access of unknown order; the hardware counts it in vmcnt.  The memory
+// clobber keeps every LDS read of the buffer it overwrites (issued earlier in program
+// order) ahead of it.
+__device__ __forceinline__ void dma16_addr(const void* addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(addr)
+               : "m0", "memory");
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Reductions over the four 16-lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
+// v_permlane16_swap with both operands holding x leaves, in every lane, x of the
+// lane in one register and x of its partner 16 lanes away in the other (rows
+// 0 <-> 1, 2 <-> 3); v_permlane32_swap does the same for the two half-waves.
+// Issued through inline assembly with both registers as in/out operands: the
+// compiler (ROCm 7.2) folds the two results of the swap builtins into one, which
+// drops the partner's value.  The s_nop covers the VALU-write -> permlane-read
+// hazard, which the compiler does not track through inline assembly.
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float group4_max(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  a = b = fmaxf(a, b);
+  swap32(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float group4_sum(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  a = b = a + b;
+  swap32(a, b);
+  return a + b;
+}
+
+__device__ __forceinline__ float merge_weight(float m, float mx) {
+  return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
+}
+
+template <int W, int S>
+__global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
+  constexpr int kThreads = W * 64;
+  constexpr int kWaveLds = S * kStageBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[W * kWaveLds];
+  __shared__ int last_flag;
+
+  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c = lane & 15;   // column (q head within the group)
+  const int q4 = lane >> 4;  // 16-lane group
+
+  int ctx = p.seqlens[b];
+  ctx = max(0, min(ctx, p.max_keys));
+  const int n_splits = max(1, (ctx + p.key_chunk - 1) / p.key_chunk);
+  if (split >= n_splits) return;  // uniform over the workgroup, before any barrier
+  const int kb = split * p.key_chunk;
+  const int ke = min(ctx, kb + p.key_chunk);
+  const int wchunk = p.key_chunk / W;
+  const int wkb = kb + wave * wchunk;
+  const int wke = min(ke, wkb + wchunk);
+  const int n_tiles = wke > wkb ? (wke - wkb + kTileKeys - 1) / kTileKeys : 0;
+
+  // Block ids of the wave's pages: lane i holds the id of page first_page + i.
+  const int first_page = wkb / p.page_size;
+  int blk_reg = -1;
+  {
+    const int pg = first_page + lane;
+    if (n_tiles > 0 && pg < p.bt_cols && lane < kMaxPagesPerWave)
+      blk_reg = p.block_table[(int64_t)b * p.bt_row_stride + pg];
+  }
+
+  // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[head c][32 kk + 8 q4 .. + 8].
+  const bool col_ok = c < p.group;
+  bf16x8 qf[4];
+  {
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_row_stride +
+                           (int64_t)(g * p.group + (col_ok ? c : 0)) * kHeadDim + 8 * q4;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4v w = *reinterpret_cast<const u32x4v*>(qrow + 32 * kk);
+      if (!col_ok) w = u32x4v{0u, 0u, 0u, 0u};
+      qf[kk] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+
+  uint8_t* wbuf = lds + wave * kWaveLds;
+  const char* kbase = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim);
+  const char* vbase = reinterpret_cast<const char*>(p.v + (int64_t)g * kHeadDim);
+  const int64_t row_bytes = p.cache_row_stride * 2;
+  const char* zero = reinterpret_cast<const char*>(kZeroRow);
+
+  // Tile t of the wave -> stage st.  Instruction j moves rows 4j .. 4j+3 (1 KB): lane i
+  // fills slot i % 16 of row 4j + i / 16, so it loads that row's chunk
+  // (i % 16) ^ swizzle(row).  A 32-key tile lies inside one page (page_size % 32 == 0).
+  auto dma_tile = [&](int t, int st) __attribute__((always_inline)) {
+    const int kt = wkb + t * kTileKeys;
+    const int pg = kt / p.page_size;
+    const int blk = __builtin_amdgcn_readlane(blk_reg, pg - first_page);
+    const bool blk_ok = blk >= 0 && blk < p.num_blocks;
+    const int64_t row0 = (int64_t)blk * p.page_size + (kt - pg * p.page_size);
+    uint8_t* kdst = wbuf + st * kStageBytes;
+    uint8_t* vdst = kdst + kTileBytes;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * j + (lane >> 4);
+      const bool ok = blk_ok && kt + r < wke;
+      const int kc = (lane & 15) ^ swz_k(r);
+      const int vc = (lane & 15) ^ swz_v(r);
+      const char* ks = ok ? kbase + (row0 + r) * row_bytes + kc * 16 : zero + kc * 16;
+      const char* vs = ok ? vbase + (row0 + r) * row_bytes + vc * 16 : zero + vc * 16;
+      dma16_addr(ks, lds_u32(kdst + j * 1024));
+      dma16_addr(vs, lds_u32(vdst + j * 1024));
+    }
+  };
+
+  // V^T operand offsets (ds_read_b64_tr_b16): in 16-lane group q4, lane 4f + r reads
+  // dims 16 mb + 4r .. +4 of row 4 q4 + f (+16 for the second read); the transpose
+  // hands lane j of the group dim 16 mb + j of those 4 rows.
+  const int vf = (lane & 15) >> 2, vr = lane & 3;
+  auto voff = [&](int mb, int second) __attribute__((always_inline)) {
+    const int row = 4 * q4 + vf + 16 * second;
+    const int chunk = 2 * mb + (vr >> 1);
+    return row * 256 + ((chunk ^ swz_v(row)) << 4) + 8 * (vr & 1);
+  };
+
+  f32x4 o[8];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) o[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (u < n_tiles) dma_tile(u, u);
+  int st = 0;  // stage of tile t
+  for (int t = 0; t < n_tiles; ++t) {
+    // Tile t + S - 1 goes into the stage tile t - 1 used (read in the previous step).
+    if (t + S - 1 < n_tiles) dma_tile(t + S - 1, st == 0 ? S - 1 : st - 1);
+    // Tiles issued after tile t may stay in flight; tile t has landed.
+    const int ahead = min(S - 1, n_tiles - 1 - t);
+    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint8_t* kb_ = wbuf + st * kStageBytes;
+    st = st + 1 == S ? 0 : st + 1;
+    const uint8_t* vb_ = kb_ + kTileBytes;
+    const int kt = wkb + t * kTileKeys;
+
+    // S^T for keys 16 blk + 4 q4 + i
+    f32x4 s[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      s[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int r = 16 * blk + c;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kb_ + r * 256 + (((4 * kk + q4) ^ swz_k(r)) << 4));
+        s[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[kk], s[blk], 0, 0, 0);
+      }
+    }
+    float x[8];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kt + 16 * blk + 4 * q4 + i;
+        x[4 * blk + i] = key < wke ? s[blk][i] * p.scale_log2 : -INFINITY;
+      }
+    float mx = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+    mx = group4_max(mx);
+    const float m_new = fmaxf(m_run, mx);  // finite: the tile holds at least one key of the wave
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float pr[8], psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pr[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+      psum += pr[i];
+    }
+    l_run = l_run * alpha + psum;
+    // P^T operand: k-element e < 4 is key 4 q4 + e, e >= 4 is key 16 + 4 q4 + (e - 4).
+    const u32x4v pw = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
+                       pack_bf16x2(pr[6], pr[7])};
+    const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(lds_u32(vb_) + voff(mb, 0)));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(lds_u32(vb_) + voff(mb, 1)));
+      const u32x2v lw = __builtin_bit_cast(u32x2v, lo), hw = __builtin_bit_cast(u32x2v, hi);
+      const u32x4v vw = {lw[0], lw[1], hw[0], hw[1]};
+      o[mb] *= alpha;
+      o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), pb, o[mb], 0, 0, 0);
+    }
+  }
+
+  // ---- merge the W waves through LDS (each wave reuses its own region) -------------
+  const float l_tot = group4_sum(l_run);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's DMAs and reads are done
+  float* lo_ = reinterpret_cast<float*>(wbuf);                  // [kCols][kHeadDim] fp32
+  float* lml = reinterpret_cast<float*>(wbuf + kCols * kHeadDim * 4);  // [kCols][2]
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+    *reinterpret_cast<f32x4*>(lo_ + c * kHeadDim + 16 * mb + 4 * q4) = o[mb];
+  if (q4 == 0) {
+    lml[2 * c] = m_run;
+    lml[2 * c + 1] = l_tot;
+  }
+  __syncthreads();
+
+  // Thread (c2, piece): column c2, dims 8 piece .. 8 piece + 7, pieces strided by W * 4.
+  const int c2 = tid & 15;
+  float mw[W], lw[W];
+  float mmax = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const float* ml = reinterpret_cast<const float*>(lds + w * kWaveLds + kCols * kHeadDim * 4);
+    mw[w] = ml[2 * c2];
+    lw[w] = ml[2 * c2 + 1];
+    mmax = fmaxf(mmax, mw[w]);
+  }
+  float lsum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) lsum += merge_weight(mw[w], mmax) * lw[w];
+  constexpr int kPieces = 4 / W;  // 8-dim pieces per thread (16 per column, 4W threads per column)
+  float acc[kPieces][8];
+#pragma unroll
+  for (int pc = 0; pc < kPieces; ++pc) {
+    const int d0 = ((tid >> 4) + pc * (W * 4)) * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[pc][i] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float wt = merge_weight(mw[w], mmax);
+      const float* src = reinterpret_cast<const float*>(lds + w * kWaveLds) + c2 * kHeadDim + d0;
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(src);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[pc][i] += wt * a0[i];
+        acc[pc][4 + i] += wt * a1[i];
+      }
+    }
+  }
+
+  if (n_splits == 1) {
+    if (c2 < p.group) {
+      const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+#pragma unroll
+      for (int pc = 0; pc < kPieces; ++pc) {
+        const int d0 = ((tid >> 4) + pc * (W * 4)) * 8;
+        const float* a = acc[pc];
+        const u32x4v w = {pack_bf16x2(a[0] * inv, a[1] * inv), pack_bf16x2(a[2] * inv, a[3] * inv),
+                          pack_bf16x2(a[4] * inv, a[5] * inv), pack_bf16x2(a[6] * inv, a[7] * inv)};
+        *reinterpret_cast<u32x4v*>(p.out + (int64_t)b * p.out_row_stride +
+                                   (int64_t)(g * p.group + c2) * kHeadDim + d0) = w;
+      }
+    }
+    return;
+  }
+
+  // ---- several chunks: publish this chunk's (O, m, l), the last one merges ----------
+  // The partials cross workgroups (and XCDs, whose L2 caches are not coherent with
+  // each other) as agent-scope atomic stores and loads, which the compiler emits as
+  // single sc1 accesses, coherent at agent scope.  Each thread waits until its
+  // stores have completed before the barrier that precedes the ticket, so the
+  // ticket order orders them.  (An agent-scope release/acquire fence would do
+  // the same by writing back and invalidating the whole L2 in every workgroup.)
+  // Only the group's columns are stored: [pair][split][group][kHeadDim] and
+  // [pair][split][group][2].
+  const int64_t pair = (int64_t)b * p.num_heads_kv + g;
+  const int64_t grid_splits = gridDim.x;
+  const int grp = p.group;
+  if (c2 < grp) {
+#pragma unroll
+    for (int pc = 0; pc < kPieces; ++pc) {
+      const int d0 = ((tid >> 4) + pc * (W * 4)) * 8;
+      float* po = p.part_o + ((pair * grid_splits + split) * grp + c2) * kHeadDim + d0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        __hip_atomic_store(po + i, acc[pc][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if ((tid >> 4) == 0) {
+      float* pm = p.part_ml + ((pair * grid_splits + split) * grp + c2) * 2;
+      __hip_atomic_store(pm, mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pm + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials have landed
+  __syncthreads();
+  if (tid == 0)
+    last_flag = __hip_atomic_fetch_add(p.counters + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                (unsigned)(n_splits - 1);
+  __syncthreads();
+  if (!last_flag) return;
+
+  // Online merge over the chunks, kMergeBatch chunks of loads in flight at a time;
+  // thread (col, 4 dims) over the group's columns.
+  auto ld = [](const float* a) __attribute__((always_inline)) {
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  constexpr int kMergeBatch = 16;
+  for (int idx = tid; idx < grp * (kHeadDim / 4); idx += kThreads) {
+    const int col = idx / (kHeadDim / 4);
+    const int dd = (idx - col * (kHeadDim / 4)) * 4;
+    float run_m = -INFINITY, run_l = 0.0f, tot[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+      float ms[kMergeBatch], ls[kMergeBatch], a[kMergeBatch][4];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int sx = min(s0 + u, n_splits - 1);  // clamped: extra slots get weight 0 below
+        const float* pm = p.part_ml + ((pair * grid_splits + sx) * grp + col) * 2;
+        const float* po = p.part_o + ((pair * grid_splits + sx) * grp + col) * kHeadDim + dd;
+        ms[u] = ld(pm);
+        ls[u] = ld(pm + 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[u][i] = ld(po + i);
+      }
+      float bm = run_m;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u)
+        if (s0 + u < n_splits) bm = fmaxf(bm, ms[u]);
+      const float rescale = merge_weight(run_m, bm);
+      run_l *= rescale;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tot[i] *= rescale;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const float wt = s0 + u < n_splits ? merge_weight(ms[u], bm) : 0.0f;
+        run_l += wt * ls[u];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tot[i] += wt * a[u][i];
+      }
+      run_m = bm;
+    }
+    const float inv = run_l > 0.0f ? 1.0f / run_l : 0.0f;
+    const u32x2v w = {pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv)};
+    *reinterpret_cast<u32x2v*>(p.out + (int64_t)b * p.out_row_stride + (int64_t)(g * grp + col) * kHeadDim + dd) = w;
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+}
+
+}  // namespace
+}  // namespace decode
+}  // namespace vlc
+
+using vlc::decode::kCols;
+using vlc::decode::kHeadDim;
+using vlc::decode::kMaxPagesPerWave;
+using vlc::decode::kTileKeys;
+using vlc::decode::kWgKeys;
+using vlc::decode::pipeline_code;
+
+namespace {
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+// Workspace layout: counters [B*Hkv] u32 | part_ml [B*Hkv][splits][kCols][2] f32 |
+// part_o [B*Hkv][splits][kCols][kHeadDim] f32.
+void ws_layout(int batch, int num_heads_kv, int grid_splits, int64_t* off_ml, int64_t* off_o, int64_t* total) {
+  const int64_t pairs = (int64_t)batch * num_heads_kv;
+  *off_ml = align256(pairs * 4);
+  *off_o = *off_ml + align256(pairs * grid_splits * kCols * 2 * 4);
+  *total = *off_o + pairs * grid_splits * kCols * kHeadDim * 4;
+}
+// Waves per workgroup of a pipeline code, 0 if the code is not one the library has.
+int pipeline_waves(int code) {
+  switch (code) {
+    case pipeline_code(4, 2): return 4;
+    case pipeline_code(2, 2): case pipeline_code(2, 3): case pipeline_code(2, 4): return 2;
+    case pipeline_code(1, 4): return 1;
+    default: return 0;
+  }
+}
+// Workgroups that fit one CU (160 KB of LDS, 16 KB per stage and wave).
+int wgs_per_cu(int code) { return std::max(1, 160 / (16 * (code / 16) * (code % 16))); }
+}  // namespace
+
+VLC_API int vlc_decode_attn_plan(int batch, int num_heads_q, int num_heads_kv, int head_dim, int page_size,
+                                 int max_seqlen_k, int num_cus, int num_splits, int pipeline,
+                                 int32_t* key_chunk, int32_t* grid_splits, int32_t* pipeline_out,
+                                 int64_t* workspace_bytes) {
+  if (!key_chunk || !grid_splits || !pipeline_out || !workspace_bytes) return VLC_ERR_INVALID;
+  if (batch < 0 || num_heads_kv <= 0 || num_heads_q <= 0 || num_heads_q % num_heads_kv != 0 ||
+      max_seqlen_k < 0 || page_size <= 0)
+    return VLC_ERR_INVALID;
+  if (head_dim != kHeadDim || num_heads_q / num_heads_kv > kCols || page_size % kTileKeys != 0)
+    return VLC_ERR_UNSUPPORTED;
+  if (pipeline == 0) pipeline = pipeline_code(2, 4);
+  const int waves = pipeline_waves(pipeline);
+  if (waves == 0) return VLC_ERR_UNSUPPORTED;
+  if (num_cus <= 0) num_cus = 256;
+  const int64_t pairs = std::max<int64_t>(1, (int64_t)batch * num_heads_kv);
+  int splits = num_splits;
+  if (splits <= 0) {
+    // One wave of workgroups over the CUs, at most 32 chunks to merge per pair.
+    const int64_t slots = (int64_t)num_cus * wgs_per_cu(pipeline);
+    splits = (int)std::max<int64_t>(1, std::min<int64_t>(32, slots / pairs));
+  }
+  int64_t chunk = ((int64_t)std::max(1, max_seqlen_k) + splits - 1) / splits;
+  chunk = (chunk + kWgKeys - 1) / kWgKeys * kWgKeys;
+  // A wave's share of the chunk must fit the block ids it keeps in a register.
+  const int64_t max_chunk = (int64_t)waves * (kMaxPagesPerWave - 1) * page_size;
+  if (chunk > max_chunk) chunk = max_chunk / kWgKeys * kWgKeys;
+  if (chunk <= 0 || chunk > (1 << 30)) return VLC_ERR_UNSUPPORTED;
+  const int64_t gs = std::max<int64_t>(1, ((int64_t)max_seqlen_k + chunk - 1) / chunk);
+  if (gs > 65535) return VLC_ERR_UNSUPPORTED;
+  int64_t off_ml, off_o, total;
+  ws_layout(batch, num_heads_kv, (int)gs, &off_ml, &off_o, &total);
+  *key_chunk = (int32_t)chunk;
+  *grid_splits = (int32_t)gs;
+  *pipeline_out = pipeline;
+  *workspace_bytes = total;
+  return VLC_OK;
+}
+
+VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                            int64_t cache_row_stride, int page_size, int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_row_stride, int bt_cols,
+                            const int32_t* cache_seqlens, int batch, int num_heads_q, int num_heads_kv,
+                            int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
+                            void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+  using namespace vlc;
+  if (batch < 0 || num_heads_kv <= 0 || num_heads_q <= 0 || num_heads_q % num_heads_kv != 0)
+    return VLC_ERR_INVALID;
+  if (head_dim != kHeadDim || num_heads_q / num_heads_kv > kCols || page_size <= 0 ||
+      page_size % kTileKeys != 0)
+    return VLC_ERR_UNSUPPORTED;
+  const int waves = pipeline_waves(pipeline);
+  if (waves == 0) return VLC_ERR_INVALID;
+  if (batch == 0) return VLC_OK;
+  if (batch > 65535 || num_heads_kv > 65535) return VLC_ERR_UNSUPPORTED;  // grid z / y
+  if (!q || !k_cache || !v_cache || !block_table || !cache_seqlens || !out || !workspace) return VLC_ERR_INVALID;
+  if (key_chunk <= 0 || key_chunk % kWgKeys != 0 || grid_splits <= 0 || grid_splits > 65535 || bt_cols <= 0)
+    return VLC_ERR_INVALID;
+  if ((int64_t)key_chunk > (int64_t)waves * (kMaxPagesPerWave - 1) * page_size) return VLC_ERR_INVALID;
+  const int64_t group = num_heads_q / num_heads_kv;
+  if (q_row_stride < num_heads_q * (int64_t)kHeadDim || out_row_stride < num_heads_q * (int64_t)kHeadDim ||
+      cache_row_stride < num_heads_kv * (int64_t)kHeadDim || bt_row_stride < bt_cols || num_blocks <= 0)
+    return VLC_ERR_INVALID;
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || q_row_stride % 8 ||
+      out_row_stride % 8 || cache_row_stride % 8 || !aligned16(workspace))
+    return VLC_ERR_INVALID;
+  int64_t off_ml, off_o, total;
+  ws_layout(batch, num_heads_kv, grid_splits, &off_ml, &off_o, &total);
+  if (workspace_bytes < total) return VLC_ERR_WORKSPACE;
+  decode::Params p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k_cache);
+  p.v = static_cast<const uint16_t*>(v_cache);
+  p.block_table = block_table;
+  p.seqlens = cache_seqlens;
+  p.out = static_cast<uint16_t*>(out);
+  p.counters = static_cast<uint32_t*>(workspace);
+  p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + off_ml);
+  p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + off_o);
+  p.q_row_stride = q_row_stride;
+  p.out_row_stride = out_row_stride;
+  p.cache_row_stride = cache_row_stride;
+  p.bt_row_stride = bt_row_stride;
+  p.num_blocks = num_blocks;
+  p.page_size = page_size;
+  p.bt_cols = bt_cols;
+  p.group = (int)group;
+  p.num_heads_kv = num_heads_kv;
+  p.key_chunk = key_chunk;
+  const int64_t cover = std::min<int64_t>((int64_t)bt_cols * page_size, (int64_t)grid_splits * key_chunk);
+  p.max_keys = (int)std::min<int64_t>(cover, INT32_MAX);
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  const dim3 grid(grid_splits, num_heads_kv, batch);
+  hipStream_t st = as_stream(stream);
+  switch (pipeline) {
+    case pipeline_code(4, 2): hipLaunchKernelGGL((decode::decode_attn_kernel<4, 2>), grid, dim3(256), 0, st, p); break;
+    case pipeline_code(2, 2): hipLaunchKernelGGL((decode::decode_attn_kernel<2, 2>), grid, dim3(128), 0, st, p); break;
+    case pipeline_code(2, 3): hipLaunchKernelGGL((decode::decode_attn_kernel<2, 3>), grid, dim3(128), 0, st, p); break;
+    case pipeline_code(2, 4): hipLaunchKernelGGL((decode::decode_attn_kernel<2, 4>), grid, dim3(128), 0, st, p); break;
+    default: hipLaunchKernelGGL((decode::decode_attn_kernel<1, 4>), grid, dim3(64), 0, st, p); break;
+  }
+  return launch_status();
+}

@@ -7,7 +7,8 @@ prepare_sample, run_model, run, allocate_kv_cache, exit.  Differences:
     to the image's new rotary position (without deltas it is the reference's
     plain copy, bit for bit);
   * prepare_prefill builds the step's attention work plan once (host lists are
-    at hand) and passes it through the Context to every layer;
+    at hand) and passes it through the Context to every layer; prepare_decode
+    passes a decode launch plan (cached per batch size and context bucket);
   * positions are M-RoPE [3, N] when the model config has mrope_section and
     use_mrope is set, else the reference's 1-D positions;
   * host preparation is vectorised (numpy) instead of per-token Python loops;
@@ -69,6 +70,7 @@ class ModelRunner:
         self.num_heads = hf.num_attention_heads
         self.head_dim = hf.head_dim
         self._logit_indices = None
+        self._decode_plans: dict = {}
         self.allocate_kv_cache()
 
     def call(self, method_name, *args):
@@ -210,14 +212,31 @@ class ModelRunner:
             bt[i, :len(s.block_table)] = s.block_table
         cu_q = list(range(n + 1))
         cu_k = [0] + np.cumsum(lens).tolist()
-        plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
-                                      self.device)
+        plan = dplan = None
+        if kernels.decode_supported(self.num_heads, self.num_kv_heads, self.head_dim, self.block_size):
+            dplan = self._decode_plan(n, int(lens.max()))
+        else:
+            plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
+                                          self.device)
         set_context(False, _h2d(np.asarray(cu_q), torch.int32, self.device),
                     _h2d(np.asarray(cu_k), torch.int32, self.device), 1, int(lens.max()),
                     _h2d(slot, torch.int32, self.device), _h2d(lens, torch.int32, self.device),
                     _h2d(bt, torch.int32, self.device), attn_plan=plan, cu_seqlens_q_host=cu_q,
-                    cu_seqlens_k_host=cu_k)
+                    cu_seqlens_k_host=cu_k, decode_plan=dplan)
         return _h2d(input_ids, torch.int64, self.device), _h2d(pos, torch.int64, self.device)
+
+    def _decode_plan(self, batch: int, max_len: int):
+        """Decode launch plan for this batch size, sized for contexts up to the next multiple of
+        1024 tokens and reused across steps (its workspace counters return to zero after
+        every call)."""
+        cap = -(-max(max_len, 1) // 1024) * 1024
+        key = (batch, cap)
+        plan = self._decode_plans.get(key)
+        if plan is None:
+            plan = kernels.plan_decode(batch, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size,
+                                       cap, self.device)
+            self._decode_plans[key] = plan
+        return plan
 
     def prepare_sample(self, seqs: list[Sequence]):
         return _h2d(np.array([s.temperature for s in seqs], dtype=np.float32), torch.float32, self.device)

@@ -352,3 +352,103 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         ws.numel() if ws is not None else 0, _stream(q))
     _lib.check("vlc_varlen_attn_fwd", st)
     return out
+
+
+# --------------------------------------------------------------------------- decode attention
+@dataclass
+class DecodePlan:
+    """Launch shape and workspace of vlc_decode_attn for one upper bound of the context length.
+
+    The workspace's first batch * Hkv words are ticket counters: zero at
+    allocation, and every call leaves them zero, so one plan serves every layer
+    and step whose lengths stay within max_seqlen_k.
+    """
+    batch: int
+    num_heads_q: int
+    num_heads_kv: int
+    page_size: int
+    max_seqlen_k: int
+    key_chunk: int
+    grid_splits: int
+    pipeline: int
+    workspace: torch.Tensor
+
+
+def decode_supported(num_heads_q: int, num_heads_kv: int, head_dim: int, page_size: int) -> bool:
+    """Shapes vlc_decode_attn takes: head_dim 128, at most 16 q heads per kv head, page_size % 32 == 0."""
+    return (head_dim == HEAD_DIM and num_heads_q % num_heads_kv == 0 and num_heads_q // num_heads_kv <= 16
+            and page_size % 32 == 0)
+
+
+def plan_decode(batch: int, num_heads_q: int, num_heads_kv: int, head_dim: int, page_size: int,
+                max_seqlen_k: int, device, num_cus: int | None = None, num_splits: int = 0,
+                pipeline: int = 0) -> DecodePlan:
+    """Size a decode launch (vlc_decode_attn_plan) and allocate its zeroed workspace.
+
+    pipeline: kernel shape, 16 * waves per workgroup + stages per wave (0x42, 0x22,
+    0x23, 0x24, 0x14), 0 = the library's choice.
+    """
+    lib = _lib.load()
+    device = torch.device(device)
+    if num_cus is None:
+        num_cus = _num_cus(device) if device.type == "cuda" else 256
+    chunk = ctypes.c_int32(0)
+    splits = ctypes.c_int32(0)
+    pipe = ctypes.c_int32(0)
+    ws = ctypes.c_int64(0)
+    st = lib.vlc_decode_attn_plan(batch, num_heads_q, num_heads_kv, head_dim, page_size, int(max_seqlen_k),
+                                  num_cus, num_splits, pipeline, ctypes.byref(chunk), ctypes.byref(splits),
+                                  ctypes.byref(pipe), ctypes.byref(ws))
+    _lib.check("vlc_decode_attn_plan", st)
+    workspace = torch.zeros(max(ws.value, 16), dtype=torch.uint8, device=device)
+    return DecodePlan(batch, num_heads_q, num_heads_kv, page_size, int(max_seqlen_k), chunk.value, splits.value,
+                      pipe.value, workspace)
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_seqlens: torch.Tensor,
+                     block_table: torch.Tensor, softmax_scale: float, plan: DecodePlan | None = None,
+                     max_seqlen_k: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged GQA decode attention, one query per sequence (vlc_decode_attn).
+
+    q: [B, Hq, 128] bf16 (any row stride between sequences); k_cache/v_cache:
+    [num_blocks, page, Hkv, 128]; cache_seqlens: int32 [B] on the device;
+    block_table: int32 [B, max_blocks].  The plan must cover the longest length
+    (max_seqlen_k); without one it is built here from max_seqlen_k, or from
+    cache_seqlens (a device-to-host copy).  Returns [B, Hq, 128].
+    """
+    _require_device("decode_attention", q, k_cache, v_cache, cache_seqlens, block_table)
+    B, hq = q.shape[0], q.shape[1]
+    hkv = k_cache.shape[-2]
+    _check_rows("q", q, hq)
+    _check_rows("k_cache", k_cache, hkv)
+    _check_rows("v_cache", v_cache, hkv)
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, page, Hkv, hd]")
+    if k_cache.stride(0) != k_cache.shape[1] * k_cache.stride(1) or v_cache.stride(1) != k_cache.stride(1) \
+            or v_cache.stride(0) != k_cache.stride(0):
+        raise ValueError("paged caches must have contiguous pages and equal strides")
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.numel() != B:
+        raise ValueError("cache_seqlens must be int32 [B]")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
+            or block_table.stride(1) != 1:
+        raise ValueError("block_table must be int32 [B, max_blocks] with contiguous rows")
+    page, nblocks = k_cache.shape[1], k_cache.shape[0]
+    if plan is None:
+        if max_seqlen_k is None:
+            max_seqlen_k = int(cache_seqlens.max().item()) if B else 0
+        plan = plan_decode(B, hq, hkv, HEAD_DIM, page, max_seqlen_k, q.device)
+    if (plan.batch, plan.num_heads_q, plan.num_heads_kv, plan.page_size) != (B, hq, hkv, page):
+        raise ValueError("decode plan does not match the call")
+    if out is None:
+        out = torch.empty(B, hq, HEAD_DIM, dtype=torch.bfloat16, device=q.device)
+    elif out.shape != (B, hq, HEAD_DIM) or out.dtype != torch.bfloat16 or out.stride(-1) != 1 \
+            or out.stride(1) != HEAD_DIM:
+        raise ValueError("out must be bf16 [B, Hq, 128] with contiguous head rows")
+    ws = plan.workspace
+    st = _lib.load().vlc_decode_attn(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(1), page, nblocks,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], cache_seqlens.data_ptr(), B, hq, hkv,
+        HEAD_DIM, float(softmax_scale), plan.key_chunk, plan.grid_splits, plan.pipeline, out.data_ptr(), out.stride(0),
+        ws.data_ptr(), ws.numel(), _stream(q))
+    _lib.check("vlc_decode_attn", st)
+    return out

@@ -9,7 +9,7 @@ Same public surface as layers/attention.py of the reference:
     one (the cache is read back after the scatter, :65-66) and over the fresh
     contiguous k/v otherwise; decode attends through the block table with one
     query per sequence and returns [B, 1, Hq, hd] (:71-74).
-Both attention forms run in the gfx950 varlen GQA kernel.  forward_rope(positions,
+Prefill runs in the gfx950 varlen GQA kernel, decode in the paged decode kernel.  forward_rope(positions,
 q, k, v, rotary_emb) is the fused form of the caller's sequence RoPE -> forward
 (models/qwen3.py:84-85): one kernel rotates q and k and stores k and v.
 """
@@ -91,8 +91,22 @@ class Attention(nn.Module):
             plan = _plan(context, self.num_heads, self.num_kv_heads, self.head_dim, q.device)
             return kernels.varlen_attention(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k, self.scale,
                                             True, context.block_tables, plan=plan)
-        # decode: one query per sequence against its cached context
-        plan = _plan(context, self.num_heads, self.num_kv_heads, self.head_dim, q.device)
-        o = kernels.varlen_attention(q, k_cache, v_cache, context.cu_seqlens_q, context.cu_seqlens_k, self.scale,
-                                     True, context.block_tables, plan=plan)
+        # decode: one query per sequence against its cached context (layers/attention.py:71-74)
+        if kernels.decode_supported(self.num_heads, self.num_kv_heads, self.head_dim, k_cache.shape[1]):
+            plan = context.decode_plan
+            if plan is None or plan.batch != q.shape[0] or plan.num_heads_q != self.num_heads:
+                max_k = context.max_seqlen_k or None
+                if context.cu_seqlens_k_host is not None:
+                    cu = context.cu_seqlens_k_host
+                    max_k = max((cu[i + 1] - cu[i] for i in range(len(cu) - 1)), default=0)
+                plan = kernels.plan_decode(q.shape[0], self.num_heads, self.num_kv_heads, self.head_dim,
+                                           k_cache.shape[1], max_k if max_k is not None else
+                                           int(context.context_lens.max().item()), q.device)
+                context.decode_plan = plan
+            o = kernels.decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables,
+                                         self.scale, plan=plan)
+        else:  # shapes the decode kernel does not take: the varlen kernel with one query per sequence
+            plan = _plan(context, self.num_heads, self.num_kv_heads, self.head_dim, q.device)
+            o = kernels.varlen_attention(q, k_cache, v_cache, context.cu_seqlens_q, context.cu_seqlens_k,
+                                         self.scale, True, context.block_tables, plan=plan)
         return o.unsqueeze(1)
