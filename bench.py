@@ -19,6 +19,8 @@ unfused sequence it replaces (torch eager RoPE, then the separate scatter) is
 timed after the step loop for comparison.  The rerotate is
 timed cold as well (a 512 MiB write evicts the MALL before each of 10 runs,
 median), next to a plain device copy of the same bytes timed the same way.
+The paged decode attention of the batched 7B tail (batch 4, ~13.4k context) is
+timed cold on its own (kernels.decode).
 """
 from __future__ import annotations
 
@@ -236,6 +238,82 @@ def run_ttft(ratio: float, reps: int = 2):
     return {"cold_ms": round(float(np.median(cold)), 2), "warm_ms": round(float(np.median(warm)), 2)}
 
 
+def run_decode(reps: int = 10):
+    """Paged GQA decode attention of the batched 7B request tail: batch 4 at contexts
+    13432..13435 tokens, 28 q / 4 kv heads, 256-token pages in a seeded permutation.
+
+    Each layer of a decode step reads a different layer's cache (28 x 110 MB), so
+    every read is cold: a 512 MiB read before each timed call leaves the MALL full
+    of clean lines (median of `reps`).  The same bytes are timed through the
+    varlen prefill kernel (one query per sequence) for comparison.
+    """
+    from vlcache_amd import kernels
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    B, hq, hkv, page = 4, 28, 4, 256
+    lens = [13432 + i for i in range(B)]
+    nbs = [-(-n // page) for n in lens]
+    nb = sum(nbs)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(7)).to(torch.int32)
+    bt = torch.full((B, max(nbs)), -1, dtype=torch.int32)
+    p0 = 0
+    for i, n in enumerate(nbs):
+        bt[i, :n] = perm[p0:p0 + n]
+        p0 += n
+    bt = bt.to(dev)
+    q = torch.randn(B, hq, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    kc = torch.randn(nb, page, hkv, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(nb, page, hkv, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    plan = kernels.plan_decode(B, hq, hkv, 128, page, max(lens), dev)
+    out = torch.empty(B, hq, 128, dtype=torch.bfloat16, device=dev)
+    cu_q = list(range(B + 1))
+    cu_k = [0]
+    for n in lens:
+        cu_k.append(cu_k[-1] + n)
+    vplan = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, True, dev)
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
+    ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+    out2 = torch.empty_like(out)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def timed(fn, cold):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(reps):
+            if cold:
+                flush.view(torch.int64).sum()  # read-only: the MALL ends up holding clean lines
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    dec = lambda: kernels.decode_attention(q, kc, vc, sl, bt, 128 ** -0.5, plan=plan, out=out)
+    var = lambda: kernels.varlen_attention(q, kc, vc, cq, ck, 128 ** -0.5, True, bt, plan=vplan, out=out2)
+    nbytes = sum(lens) * hkv * 128 * 2 * 2
+    res = {"cold_us": timed(dec, True), "varlen_path_cold_us": timed(var, True)}
+    del flush
+    torch.cuda.synchronize()
+    err = (out.float() - out2.float()).abs().max().item()
+    gbps = nbytes / (res["cold_us"] * 1e-6) / 1e9
+    return {
+        "workload": "batch 4 decode, contexts 13432..13435, 28/4 heads x 128, pages of 256",
+        "bytes": nbytes, "us_per_layer": round(res["cold_us"], 2), "gbps": round(gbps, 1),
+        "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4),
+        "varlen_path_us": round(res["varlen_path_cold_us"], 2),
+        "timing": "cold (512 MiB read before each call: MALL holds clean lines), median of 10",
+        "key_chunk": plan.key_chunk, "chunks": plan.grid_splits, "pipeline": hex(plan.pipeline),
+        "max_abs_vs_varlen_path": err,
+    }
+
+
 def run_cpu_baseline(hp, budget_s: float = 20.0):
     """The oracle (fp32 torch on the host CPU) on a bounded sample of the same workload."""
     from oracle import attention as oattn
@@ -275,6 +353,7 @@ def main():
     ap.add_argument("--workload", default="cfg2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ttft", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run one plain device-to-device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -295,6 +374,7 @@ def main():
         sys.exit(2)
 
     r = run_gpu(args.steps, args.warmup, args.workload)
+    decode = run_decode() if not args.no_decode else None
     wl, hp = r["wl"], r["hp"]
     ttft = None
     if not args.no_ttft:
@@ -350,6 +430,7 @@ def main():
                         "gbps": round(r["sc_gbps"], 1), "frac_hbm_peak": round(r["sc_gbps"] / HBM_PEAK_GBPS, 4),
                         "timing": "reference-API store_kvcache, timed outside the step"},
             "torch_rope": {"us_per_layer": round(r["torch_rope_us"], 3)},
+            "decode": decode,
             "rerotate": None if r["rr_us"] is None else {
                 "us_all_layers": round(r["rr_us"], 2), "bytes": r["rr_bytes"], "gbps": round(r["rr_gbps"], 1),
                 "frac_hbm_peak": round(r["rr_gbps"] / HBM_PEAK_GBPS, 4),

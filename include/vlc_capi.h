@@ -194,9 +194,11 @@ int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride,
  *   *pipeline_out   the kernel shape to launch with.
  * num_splits > 0 forces the number of chunks for max_seqlen_k; 0 chooses one
  * wave of workgroups over the compute units (num_cus, 0 selects 256), at most 32
- * chunks per pair.  pipeline selects the kernel shape, 16 * waves per workgroup +
- * stages per wave, one of 0x42, 0x22, 0x23, 0x24, 0x14; 0 chooses.
- * Requires head_dim == 128, num_heads_q / num_heads_kv <= 16, page_size % 32 == 0.
+ * chunks per pair.  pipeline selects the kernel shape: 16 * waves per workgroup +
+ * stages per wave, plus 0x100 for 16-key tiles (else 32): 0x42, 0x22, 0x23, 0x24,
+ * 0x14, 0x142, 0x144, 0x182, 0x124; 0 chooses.
+ * Requires head_dim == 128, num_heads_q / num_heads_kv <= 16 and page_size a
+ * multiple of the shape's tile (16 or 32 keys).
  */
 int vlc_decode_attn_plan(int batch, int num_heads_q, int num_heads_kv, int head_dim, int page_size,
                          int max_seqlen_k, int num_cus, int num_splits, int pipeline,

@@ -453,7 +453,7 @@ def test_decode_forced_splits_repeatable(dev, splits):
     assert int(plan.workspace[:4 * 3 * 2].view(torch.int32).count_nonzero()) == 0  # counters back at zero
 
 
-@pytest.mark.parametrize("pipeline", [0x42, 0x22, 0x23, 0x24, 0x14])
+@pytest.mark.parametrize("pipeline", [0x42, 0x22, 0x23, 0x24, 0x14, 0x142, 0x144, 0x182, 0x124])
 def test_decode_pipeline_shapes(dev, pipeline):
     say(f"decode: kernel shape {pipeline:#x} (waves x stages), ragged lengths, 3 and 1 chunks")
     _decode_case(dev, [1, 95, 2500, 6000], 28, 4, seed=64, pipeline=pipeline, num_splits=3)
@@ -461,5 +461,6 @@ def test_decode_pipeline_shapes(dev, pipeline):
 
 
 def test_decode_small_pages_group7(dev):
-    say("decode: page 32, 7 q heads per kv head, lengths 95, 96, 97, 4000")
+    say("decode: page 32, 7 q heads per kv head, lengths 95, 96, 97, 4000; page 16 (16-key tiles)")
     _decode_case(dev, [95, 96, 97, 4000], 28, 4, seed=63, page=32)
+    _decode_case(dev, [15, 16, 17, 900], 16, 2, seed=66, page=16)

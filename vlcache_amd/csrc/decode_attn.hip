@@ -31,18 +31,17 @@ namespace decode {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kTileKeys = 32;                     // keys per wave tile
+constexpr int kMinTileKeys = 16;                  // page_size must be a multiple of this
 constexpr int kCols = 16;                         // MFMA columns = q heads of one kv head
-constexpr int kTileBytes = kTileKeys * kHeadDim * 2;  // 8 KB of K (or V) per tile
-constexpr int kStageBytes = 2 * kTileBytes;       // one pipeline stage: K + V of a tile
-constexpr int kWgKeys = 4 * kTileKeys;            // key chunks are multiples of this (128)
+constexpr int kWgKeys = 128;                      // key chunks are multiples of this
 constexpr int kMaxPagesPerWave = 64;              // block ids a wave keeps in a register
-constexpr int kDmaPerTile = 16;                   // global_load_lds_dwordx4 per tile (8 K + 8 V)
 
-// Pipeline shapes (waves per workgroup W, stages per wave S): a wave keeps S - 1
-// tiles in flight while it computes one, in W * S * 16 KB of LDS.  S <= 4 keeps
-// the wait count 16 (S - 1) within vmcnt's range.
-constexpr int pipeline_code(int w, int s) { return 16 * w + s; }
+// Kernel shapes: W waves per workgroup, S pipeline stages per wave, T keys per
+// tile (16 or 32).  A wave keeps S - 1 tiles in flight while it computes one, in
+// W * S * T * 512 bytes of LDS (K and V of a tile: T rows of 256 bytes each).  A
+// tile takes T / 2 LDS-DMA instructions, so S - 1 tiles ahead need a wait count of
+// (S - 1) T / 2 <= 63.
+constexpr int pipeline_code(int w, int s, int t) { return (t == 16 ? 0x100 : 0) | (16 * w + s); }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -137,14 +136,45 @@ __device__ __forceinline__ float group4_sum(float x) {
   return a + b;
 }
 
+// Waits until at most `ahead` (<= MAX) tiles of DMA instructions (D per tile) are in flight.
+template <int D, int MAX>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+  static_assert(MAX * D <= 63 && MAX <= 7, "vmcnt range");
+  if (ahead <= 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+#define VLC_WAIT_CASE(K)                                                 \
+  if constexpr (MAX >= K)                                                \
+    if (ahead == K) {                                                    \
+      asm volatile("s_waitcnt vmcnt(%0)" : : "n"(K * D) : "memory");    \
+      return;                                                            \
+    }
+  VLC_WAIT_CASE(1)
+  VLC_WAIT_CASE(2)
+  VLC_WAIT_CASE(3)
+  VLC_WAIT_CASE(4)
+  VLC_WAIT_CASE(5)
+  VLC_WAIT_CASE(6)
+  VLC_WAIT_CASE(7)
+#undef VLC_WAIT_CASE
+}
+
 __device__ __forceinline__ float merge_weight(float m, float mx) {
   return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
 }
 
-template <int W, int S>
+template <int W, int S, int T>
 __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
   constexpr int kThreads = W * 64;
+  constexpr int kTileKeys = T;
+  constexpr int kTileBytes = T * kHeadDim * 2;  // K (or V) of one tile
+  constexpr int kStageBytes = 2 * kTileBytes;
   constexpr int kWaveLds = S * kStageBytes;
+  constexpr int kDma = T / 2;                   // LDS-DMA instructions per tile (K and V)
+  constexpr int kBlocks = T / 16;               // 16-key blocks per tile
+  static_assert((S - 1) * kDma <= 63, "vmcnt range");
+  static_assert(kCols * kHeadDim * 4 + kCols * 8 <= kWaveLds, "merge scratch fits the wave's LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[W * kWaveLds];
   __shared__ int last_flag;
 
@@ -197,7 +227,7 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
 
   // Tile t of the wave -> stage st.  Instruction j moves rows 4j .. 4j+3 (1 KB): lane i
   // fills slot i % 16 of row 4j + i / 16, so it loads that row's chunk
-  // (i % 16) ^ swizzle(row).  A 32-key tile lies inside one page (page_size % 32 == 0).
+  // (i % 16) ^ swizzle(row).  A tile lies inside one page (page_size % T == 0).
   auto dma_tile = [&](int t, int st) __attribute__((always_inline)) {
     const int kt = wkb + t * kTileKeys;
     const int pg = kt / p.page_size;
@@ -207,7 +237,7 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
     uint8_t* kdst = wbuf + st * kStageBytes;
     uint8_t* vdst = kdst + kTileBytes;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < T / 4; ++j) {
       const int r = 4 * j + (lane >> 4);
       const bool ok = blk_ok && kt + r < wke;
       const int kc = (lane & 15) ^ swz_k(r);
@@ -243,63 +273,68 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
     if (t + S - 1 < n_tiles) dma_tile(t + S - 1, st == 0 ? S - 1 : st - 1);
     // Tiles issued after tile t may stay in flight; tile t has landed.
     const int ahead = min(S - 1, n_tiles - 1 - t);
-    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
-    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_tiles<kDma, S - 1>(ahead);
     const uint8_t* kb_ = wbuf + st * kStageBytes;
     st = st + 1 == S ? 0 : st + 1;
     const uint8_t* vb_ = kb_ + kTileBytes;
     const int kt = wkb + t * kTileKeys;
 
     // S^T for keys 16 blk + 4 q4 + i
-    f32x4 s[2];
+    f32x4 sacc[kBlocks];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      s[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int blk = 0; blk < kBlocks; ++blk) {
+      sacc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
       const int r = 16 * blk + c;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kb_ + r * 256 + (((4 * kk + q4) ^ swz_k(r)) << 4));
-        s[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[kk], s[blk], 0, 0, 0);
+        sacc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[kk], sacc[blk], 0, 0, 0);
       }
     }
-    float x[8];
+    float x[4 * kBlocks];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+    for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = kt + 16 * blk + 4 * q4 + i;
-        x[4 * blk + i] = key < wke ? s[blk][i] * p.scale_log2 : -INFINITY;
+        x[4 * blk + i] = key < wke ? sacc[blk][i] * p.scale_log2 : -INFINITY;
       }
     float mx = x[0];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+    for (int i = 1; i < 4 * kBlocks; ++i) mx = fmaxf(mx, x[i]);
     mx = group4_max(mx);
     const float m_new = fmaxf(m_run, mx);  // finite: the tile holds at least one key of the wave
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
-    float pr[8], psum = 0.0f;
+    float pr[4 * kBlocks], psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4 * kBlocks; ++i) {
       pr[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
       psum += pr[i];
     }
     l_run = l_run * alpha + psum;
-    // P^T operand: k-element e < 4 is key 4 q4 + e, e >= 4 is key 16 + 4 q4 + (e - 4).
-    const u32x4v pw = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
-                       pack_bf16x2(pr[6], pr[7])};
-    const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+    // P^T operand: k-element 4 blk + e is key 16 blk + 4 q4 + e, the keys the lane's
+    // S^T accumulators hold; the V^T operand reads the same keys (rows 16 blk + 4 q4 + f).
+    uint32_t pw[2 * kBlocks];
+#pragma unroll
+    for (int i = 0; i < 2 * kBlocks; ++i) pw[i] = pack_bf16x2(pr[2 * i], pr[2 * i + 1]);
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s16x4*)(lds_u32(vb_) + voff(mb, 0)));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(lds_u32(vb_) + voff(mb, 1)));
-      const u32x2v lw = __builtin_bit_cast(u32x2v, lo), hw = __builtin_bit_cast(u32x2v, hi);
-      const u32x4v vw = {lw[0], lw[1], hw[0], hw[1]};
       o[mb] *= alpha;
-      o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), pb, o[mb], 0, 0, 0);
+      if constexpr (kBlocks == 2) {
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(lds_u32(vb_) + voff(mb, 1)));
+        const u32x2v lw = __builtin_bit_cast(u32x2v, lo), hw = __builtin_bit_cast(u32x2v, hi);
+        const u32x4v vw = {lw[0], lw[1], hw[0], hw[1]};
+        const u32x4v pv = {pw[0], pw[1], pw[2], pw[3]};
+        o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), __builtin_bit_cast(bf16x8, pv),
+                                                        o[mb], 0, 0, 0);
+      } else {
+        const u32x2v pv = {pw[0], pw[1]};
+        o[mb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(lo, __builtin_bit_cast(s16x4, pv), o[mb], 0, 0, 0);
+      }
     }
   }
 
@@ -331,11 +366,11 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
   float lsum = 0.0f;
 #pragma unroll
   for (int w = 0; w < W; ++w) lsum += merge_weight(mw[w], mmax) * lw[w];
-  constexpr int kPieces = 4 / W;  // 8-dim pieces per thread (16 per column, 4W threads per column)
+  constexpr int kPieces = W <= 4 ? 4 / W : 1;  // 8-dim pieces per thread (16 per column, 4W threads each)
   float acc[kPieces][8];
 #pragma unroll
   for (int pc = 0; pc < kPieces; ++pc) {
-    const int d0 = ((tid >> 4) + pc * (W * 4)) * 8;
+    const int d0 = min((tid >> 4) + pc * (W * 4), 15) * 8;  // W = 8: threads past piece 15 repeat it
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[pc][i] = 0.0f;
 #pragma unroll
@@ -353,7 +388,7 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
   }
 
   if (n_splits == 1) {
-    if (c2 < p.group) {
+    if (c2 < p.group && (tid >> 4) < 16) {
       const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
 #pragma unroll
       for (int pc = 0; pc < kPieces; ++pc) {
@@ -380,7 +415,7 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
   const int64_t pair = (int64_t)b * p.num_heads_kv + g;
   const int64_t grid_splits = gridDim.x;
   const int grp = p.group;
-  if (c2 < grp) {
+  if (c2 < grp && (tid >> 4) < 16) {
 #pragma unroll
     for (int pc = 0; pc < kPieces; ++pc) {
       const int d0 = ((tid >> 4) + pc * (W * 4)) * 8;
@@ -456,7 +491,7 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
 using vlc::decode::kCols;
 using vlc::decode::kHeadDim;
 using vlc::decode::kMaxPagesPerWave;
-using vlc::decode::kTileKeys;
+using vlc::decode::kMinTileKeys;
 using vlc::decode::kWgKeys;
 using vlc::decode::pipeline_code;
 
@@ -470,17 +505,22 @@ void ws_layout(int batch, int num_heads_kv, int grid_splits, int64_t* off_ml, in
   *off_o = *off_ml + align256(pairs * grid_splits * kCols * 2 * 4);
   *total = *off_o + pairs * grid_splits * kCols * kHeadDim * 4;
 }
-// Waves per workgroup of a pipeline code, 0 if the code is not one the library has.
-int pipeline_waves(int code) {
-  switch (code) {
-    case pipeline_code(4, 2): return 4;
-    case pipeline_code(2, 2): case pipeline_code(2, 3): case pipeline_code(2, 4): return 2;
-    case pipeline_code(1, 4): return 1;
-    default: return 0;
-  }
+// Kernel shapes the library has: pipeline code -> (waves, stages, tile keys).
+struct Shape {
+  int code, waves, stages, tile;
+};
+constexpr Shape kShapes[] = {
+    {pipeline_code(4, 2, 32), 4, 2, 32}, {pipeline_code(2, 2, 32), 2, 2, 32}, {pipeline_code(2, 3, 32), 2, 3, 32},
+    {pipeline_code(2, 4, 32), 2, 4, 32}, {pipeline_code(1, 4, 32), 1, 4, 32}, {pipeline_code(4, 2, 16), 4, 2, 16},
+    {pipeline_code(4, 4, 16), 4, 4, 16}, {pipeline_code(8, 2, 16), 8, 2, 16}, {pipeline_code(2, 4, 16), 2, 4, 16},
+};
+const Shape* find_shape(int code) {
+  for (const Shape& sh : kShapes)
+    if (sh.code == code) return &sh;
+  return nullptr;
 }
-// Workgroups that fit one CU (160 KB of LDS, 16 KB per stage and wave).
-int wgs_per_cu(int code) { return std::max(1, 160 / (16 * (code / 16) * (code % 16))); }
+// Workgroups that fit one CU (160 KB of LDS).
+int wgs_per_cu(const Shape& sh) { return std::max(1, 160 * 1024 / (sh.waves * sh.stages * sh.tile * 512)); }
 }  // namespace
 
 VLC_API int vlc_decode_attn_plan(int batch, int num_heads_q, int num_heads_kv, int head_dim, int page_size,
@@ -491,17 +531,19 @@ VLC_API int vlc_decode_attn_plan(int batch, int num_heads_q, int num_heads_kv, i
   if (batch < 0 || num_heads_kv <= 0 || num_heads_q <= 0 || num_heads_q % num_heads_kv != 0 ||
       max_seqlen_k < 0 || page_size <= 0)
     return VLC_ERR_INVALID;
-  if (head_dim != kHeadDim || num_heads_q / num_heads_kv > kCols || page_size % kTileKeys != 0)
+  if (head_dim != kHeadDim || num_heads_q / num_heads_kv > kCols || page_size % kMinTileKeys != 0)
     return VLC_ERR_UNSUPPORTED;
-  if (pipeline == 0) pipeline = pipeline_code(2, 4);
-  const int waves = pipeline_waves(pipeline);
-  if (waves == 0) return VLC_ERR_UNSUPPORTED;
+  if (pipeline == 0) pipeline = page_size % 32 == 0 ? pipeline_code(4, 2, 32) : pipeline_code(4, 2, 16);
+  const Shape* sh = find_shape(pipeline);
+  if (!sh) return VLC_ERR_UNSUPPORTED;
+  if (page_size % sh->tile != 0) return VLC_ERR_UNSUPPORTED;
+  const int waves = sh->waves;
   if (num_cus <= 0) num_cus = 256;
   const int64_t pairs = std::max<int64_t>(1, (int64_t)batch * num_heads_kv);
   int splits = num_splits;
   if (splits <= 0) {
     // One wave of workgroups over the CUs, at most 32 chunks to merge per pair.
-    const int64_t slots = (int64_t)num_cus * wgs_per_cu(pipeline);
+    const int64_t slots = (int64_t)num_cus * wgs_per_cu(*sh);
     splits = (int)std::max<int64_t>(1, std::min<int64_t>(32, slots / pairs));
   }
   int64_t chunk = ((int64_t)std::max(1, max_seqlen_k) + splits - 1) / splits;
@@ -531,11 +573,12 @@ VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_c
   using namespace vlc;
   if (batch < 0 || num_heads_kv <= 0 || num_heads_q <= 0 || num_heads_q % num_heads_kv != 0)
     return VLC_ERR_INVALID;
-  if (head_dim != kHeadDim || num_heads_q / num_heads_kv > kCols || page_size <= 0 ||
-      page_size % kTileKeys != 0)
+  if (head_dim != kHeadDim || num_heads_q / num_heads_kv > kCols || page_size <= 0)
     return VLC_ERR_UNSUPPORTED;
-  const int waves = pipeline_waves(pipeline);
-  if (waves == 0) return VLC_ERR_INVALID;
+  const Shape* sh = find_shape(pipeline);
+  if (!sh) return VLC_ERR_INVALID;
+  if (page_size % sh->tile != 0) return VLC_ERR_UNSUPPORTED;
+  const int waves = sh->waves;
   if (batch == 0) return VLC_OK;
   if (batch > 65535 || num_heads_kv > 65535) return VLC_ERR_UNSUPPORTED;  // grid z / y
   if (!q || !k_cache || !v_cache || !block_table || !cache_seqlens || !out || !workspace) return VLC_ERR_INVALID;
@@ -578,11 +621,21 @@ VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_c
   const dim3 grid(grid_splits, num_heads_kv, batch);
   hipStream_t st = as_stream(stream);
   switch (pipeline) {
-    case pipeline_code(4, 2): hipLaunchKernelGGL((decode::decode_attn_kernel<4, 2>), grid, dim3(256), 0, st, p); break;
-    case pipeline_code(2, 2): hipLaunchKernelGGL((decode::decode_attn_kernel<2, 2>), grid, dim3(128), 0, st, p); break;
-    case pipeline_code(2, 3): hipLaunchKernelGGL((decode::decode_attn_kernel<2, 3>), grid, dim3(128), 0, st, p); break;
-    case pipeline_code(2, 4): hipLaunchKernelGGL((decode::decode_attn_kernel<2, 4>), grid, dim3(128), 0, st, p); break;
-    default: hipLaunchKernelGGL((decode::decode_attn_kernel<1, 4>), grid, dim3(64), 0, st, p); break;
+#define VLC_DECODE_CASE(W, S, T)                                                                       \
+  case pipeline_code(W, S, T):                                                                         \
+    hipLaunchKernelGGL((decode::decode_attn_kernel<W, S, T>), grid, dim3(W * 64), 0, st, p);           \
+    break;
+    VLC_DECODE_CASE(4, 2, 32)
+    VLC_DECODE_CASE(2, 2, 32)
+    VLC_DECODE_CASE(2, 3, 32)
+    VLC_DECODE_CASE(2, 4, 32)
+    VLC_DECODE_CASE(1, 4, 32)
+    VLC_DECODE_CASE(4, 2, 16)
+    VLC_DECODE_CASE(4, 4, 16)
+    VLC_DECODE_CASE(8, 2, 16)
+    VLC_DECODE_CASE(2, 4, 16)
+#undef VLC_DECODE_CASE
+    default: return VLC_ERR_INVALID;
   }
   return launch_status();
 }

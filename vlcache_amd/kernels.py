@@ -375,9 +375,9 @@ class DecodePlan:
 
 
 def decode_supported(num_heads_q: int, num_heads_kv: int, head_dim: int, page_size: int) -> bool:
-    """Shapes vlc_decode_attn takes: head_dim 128, at most 16 q heads per kv head, page_size % 32 == 0."""
+    """Shapes vlc_decode_attn takes: head_dim 128, at most 16 q heads per kv head, page_size % 16 == 0."""
     return (head_dim == HEAD_DIM and num_heads_q % num_heads_kv == 0 and num_heads_q // num_heads_kv <= 16
-            and page_size % 32 == 0)
+            and page_size % 16 == 0)
 
 
 def plan_decode(batch: int, num_heads_q: int, num_heads_kv: int, head_dim: int, page_size: int,
@@ -385,8 +385,9 @@ def plan_decode(batch: int, num_heads_q: int, num_heads_kv: int, head_dim: int, 
                 pipeline: int = 0) -> DecodePlan:
     """Size a decode launch (vlc_decode_attn_plan) and allocate its zeroed workspace.
 
-    pipeline: kernel shape, 16 * waves per workgroup + stages per wave (0x42, 0x22,
-    0x23, 0x24, 0x14), 0 = the library's choice.
+    pipeline: kernel shape, 16 * waves per workgroup + stages per wave, plus 0x100
+    for 16-key tiles (0x42, 0x22, 0x23, 0x24, 0x14, 0x142, 0x144, 0x182, 0x124),
+    0 = the library's choice.
     """
     lib = _lib.load()
     device = torch.device(device)
