@@ -398,6 +398,29 @@ def test_attention_contiguous_dense_strided_v(dev):
     assert_close(out.cpu(), ref, what="dense contiguous")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_score_gap_between_lane_halves(dev, causal):
+    """Keys 4..7 of every 8 score ~1000 above the others: the column max must cover both
+    half-waves (each holds half of a tile's keys), or exp2 of the gap overflows."""
+    say(f"attention: score gap of ~1000 between the key halves of each tile, causal={causal}")
+    hq, hkv, n = 16, 2, 300
+    g = gen(28)
+    q = torch.ones(n, hq, 128).to(torch.bfloat16)
+    k = torch.zeros(n, hkv, 128)
+    k[(torch.arange(n) % 8) >= 4] = 8.0
+    k = k.to(torch.bfloat16)
+    v = torch.randn(n, hkv, 128, generator=g).to(torch.bfloat16)
+    cu = [0, n]
+    plan = kernels.plan_attention(cu, cu, hq, hkv, 128, causal, dev)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=dev)
+    out = kernels.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cu_d, cu_d, 128 ** -0.5, causal, None,
+                                   plan=plan)
+    torch.cuda.synchronize()
+    ref = oattn.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, causal, None)
+    assert torch.isfinite(out.cpu().float()).all(), "non-finite output"
+    assert_close(out.cpu(), ref, what="score gap")
+
+
 # ----------------------------------------------------------------------------- decode attention
 def _decode_case(dev, lens, hq, hkv, seed, page=256, num_splits=0, extra_blocks=2, reps=1, pipeline=0):
     """Paged decode (one query per sequence) vs the fp32 oracle; returns the outputs of every rep."""
@@ -458,6 +481,25 @@ def test_decode_pipeline_shapes(dev, pipeline):
     say(f"decode: kernel shape {pipeline:#x} (waves x stages), ragged lengths, 3 and 1 chunks")
     _decode_case(dev, [1, 95, 2500, 6000], 28, 4, seed=64, pipeline=pipeline, num_splits=3)
     _decode_case(dev, [33, 4000], 16, 2, seed=65, pipeline=pipeline, num_splits=1)
+
+
+def test_decode_score_gap_between_lane_groups(dev):
+    say("decode: keys 4..7 of every 8 score ~1000 above the others (column max over all lane groups)")
+    B, hq, hkv, page, n = 2, 16, 2, 256, 700
+    q = torch.ones(B, hq, 128).to(torch.bfloat16)
+    kc = torch.zeros(3, page, hkv, 128)
+    kc.view(-1, hkv, 128)[(torch.arange(3 * page) % 8) >= 4] = 8.0
+    kc = kc.to(torch.bfloat16)
+    vc = torch.randn(3, page, hkv, 128, generator=gen(67)).to(torch.bfloat16)
+    bt = torch.tensor([[0, 1, 2], [2, 1, 0]], dtype=torch.int32)
+    lens = [n, 517]
+    ref = oattn.varlen_attention(q, kc, vc, [0, 1, 2], [0, n, n + 517], 128 ** -0.5, True, bt.tolist(), page)
+    plan = kernels.plan_decode(B, hq, hkv, 128, page, n, dev, num_splits=3)
+    out = kernels.decode_attention(q.to(dev), kc.to(dev), vc.to(dev), torch.tensor(lens, dtype=torch.int32,
+                                   device=dev), bt.to(dev), 128 ** -0.5, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.cpu().float()).all()
+    assert_close(out.cpu(), ref, what="decode score gap")
 
 
 def test_decode_small_pages_group7(dev):

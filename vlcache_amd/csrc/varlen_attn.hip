@@ -160,11 +160,15 @@ __device__ __forceinline__ void sync_tiles() {
 // its first operand with the lower half of its second; with both operands x the
 // two results hold, in every lane, the lane's own x and its partner's.  A VALU
 // operation, so the softmax that depends on it does not wait behind the LDS reads
-// of the products (as ds_bpermute would).
+// of the products (as ds_bpermute would).  Issued through inline assembly with
+// both registers as in/out operands: the compiler (ROCm 7.2) folds the two results
+// of the swap builtin into one, which drops the partner's value.  The s_nop covers
+// the VALU-write -> permlane-read hazard, which it does not track through inline
+// assembly.
 __device__ __forceinline__ float half_wave_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                  false, false);
-  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
 }
 
 template <int MODE>
