@@ -1,8 +1,9 @@
 """Paged KV block allocator and image-KV registry (engine/block_manager.py:8-119 of the reference).
 
-Same allocation, reference counting and partial-recompute decision.  The
-registry entry additionally records the rotary start position of the cached
-image, which the re-rotation of reused keys needs.
+Same allocation, reference counting and partial-recompute decision, taken per
+image when a prompt holds several.  The registry entry additionally records the
+rotary start position of the cached image, which the re-rotation of reused keys
+needs.
 """
 from __future__ import annotations
 
@@ -61,20 +62,27 @@ class BlockManager:
             seq.block_table.append(self._allocate_block().block_id)
 
     def try_partial_recompute(self, seq: Sequence, image_token_id: int = 151655) -> bool:
-        """Reuse decision: registry hit on the first image hash with an equal token count."""
+        """Reuse decision (engine/block_manager.py:56-75), per image.
+
+        Image k of the prompt is reused when the registry holds an entry for
+        image_hashes[k] with the same number of tokens; its first
+        R_k = ceil(ratio * N_k) tokens are recomputed (IEEE double, as the
+        reference).  With one image this is the reference's decision exactly.
+        """
         if self.recompute_ratio <= 0 or not seq.image_hashes:
             return False
         seq.find_image_token_range(image_token_id)
         if seq.image_token_range is None:
             return False
-        entry = self.image_kv_cache.get(seq.image_hashes[0])
-        if entry is None:
+        seq.image_recompute = [None] * len(seq.image_ranges)
+        for k, ((s, e), h) in enumerate(zip(seq.image_ranges, seq.image_hashes)):
+            entry = self.image_kv_cache.get(h)
+            if entry is not None and e - s == entry.img_end - entry.img_start:
+                seq.image_recompute[k] = math.ceil(self.recompute_ratio * (e - s))
+        hits = [r for r in seq.image_recompute if r is not None]
+        if not hits:
             return False
-        img_start, img_end = seq.image_token_range
-        n = img_end - img_start
-        if n != entry.img_end - entry.img_start:
-            return False
-        seq.num_recompute_tokens = math.ceil(self.recompute_ratio * n)  # IEEE double, as the reference
+        seq.num_recompute_tokens = hits[0]
         seq.is_partial_recompute = True
         return True
 
@@ -82,17 +90,18 @@ class BlockManager:
         return self.image_kv_cache.get(image_hash)
 
     def store_image_kv(self, seq: Sequence):
+        """Register the KV of each image of a prefilled sequence under its hash."""
         if not seq.image_hashes or seq.image_token_range is None:
             return
-        image_hash = seq.image_hashes[0]
-        img_start, img_end = seq.image_token_range
-        old = self.image_kv_cache.get(image_hash)
-        if old is not None:
-            self._release_image_blocks(old)
-        for i in range(img_start // self.block_size, (img_end - 1) // self.block_size + 1):
-            self.blocks[seq.block_table[i]].ref_count += 1
-        self.image_kv_cache[image_hash] = ImageKVEntry(list(seq.block_table), img_start, img_end,
-                                                       seq.image_rope_start)
+        ranges = seq.image_ranges or [seq.image_token_range]
+        starts = seq.image_rope_starts or [seq.image_rope_start] * len(ranges)
+        for (img_start, img_end), image_hash, rope in zip(ranges, seq.image_hashes, starts):
+            old = self.image_kv_cache.get(image_hash)
+            for i in range(img_start // self.block_size, (img_end - 1) // self.block_size + 1):
+                self.blocks[seq.block_table[i]].ref_count += 1
+            if old is not None:
+                self._release_image_blocks(old)
+            self.image_kv_cache[image_hash] = ImageKVEntry(list(seq.block_table), img_start, img_end, rope)
 
     def _release_image_blocks(self, entry: ImageKVEntry):
         for i in range(entry.img_start // self.block_size, (entry.img_end - 1) // self.block_size + 1):

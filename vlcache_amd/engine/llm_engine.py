@@ -8,7 +8,8 @@ image KV for reuse (:58-120); generate() returns
 [{text, token_ids, vit_time, ttft}] (:125-167).
 
 The reused-KV copy also re-rotates K from the cached image's rotary start to
-the new one (the reference copies the keys unchanged, :75-89).
+the new one (the reference copies the keys unchanged, :75-89).  A prompt may
+hold several images; each is reused or computed on its own.
 """
 from __future__ import annotations
 
@@ -33,6 +34,49 @@ def image_hash(pixel_values: torch.Tensor, grid_thw: torch.Tensor) -> int:
     h.update(grid_thw.cpu().numpy().tobytes())
     h.update(pixel_values.cpu().numpy().tobytes())
     return h.intdigest()
+
+
+def image_kv_copy_plan(seqs: list[Sequence], block_manager):
+    """Slots of the reused image KV of a prefill step (engine/llm_engine.py:58-89).
+
+    For image k of a partially recomputed sequence with a registry hit, positions
+    p in [start_k + R_k, end_k) take the rows of the cached entry's positions
+    entry.img_start + (p - start_k).  Returns (old_slots, new_slots, deltas,
+    seg_of_token) for ModelRunner.copy_image_kv - one launch for every image of
+    every sequence, image k being rotation segment k with delta = its new rotary
+    start - the cached one (deltas None when a rotary start is unknown) - or None
+    when nothing is reused.
+    """
+    bs = block_manager.block_size
+    olds, news, segs, deltas = [], [], [], []
+    have_rope = True
+    for seq in seqs:
+        if not seq.is_partial_recompute:
+            continue
+        sbt = np.asarray(seq.block_table, dtype=np.int64)
+        starts = seq.image_rope_starts or [seq.image_rope_start] * len(seq.image_ranges)
+        for (img_start, img_end), r, h, rope in zip(seq.image_ranges, seq.image_recompute, seq.image_hashes, starts):
+            if r is None:
+                continue
+            entry = block_manager.get_image_kv_entry(h)
+            if entry is None:
+                continue
+            p = np.arange(img_start + r, img_end, dtype=np.int64)
+            if p.size == 0:
+                continue
+            old_p = entry.img_start + (p - img_start)
+            ebt = np.asarray(entry.block_table, dtype=np.int64)
+            olds.append(ebt[old_p // bs] * bs + old_p % bs)
+            news.append(sbt[p // bs] * bs + p % bs)
+            segs.append(np.full(p.size, len(deltas), dtype=np.int32))
+            if entry.rope_start is None or rope is None:
+                have_rope = False
+                deltas.append([0, 0, 0])
+            else:
+                deltas.append([a - b for a, b in zip(rope, entry.rope_start)])
+    if not olds:
+        return None
+    return np.concatenate(olds), np.concatenate(news), (deltas if have_rope else None), np.concatenate(segs)
 
 
 class LLMEngine:
@@ -79,6 +123,7 @@ class LLMEngine:
                                                  hf.spatial_merge_size)
             seq.rope_positions = pos
             seq.image_rope_start = starts[0]
+            seq.image_rope_starts = list(starts)
             seq.rope_delta = delta
         else:
             seq.rope_positions = None
@@ -86,30 +131,13 @@ class LLMEngine:
             if seq.image_token_range is not None:
                 s = seq.image_token_range[0]
                 seq.image_rope_start = (s, s, s)
+                seq.image_rope_starts = [(a, a, a) for a, _ in seq.image_ranges]
                 seq.image_token_range = None  # decided again by the scheduler
 
     def _do_image_kv_copy(self, seqs: list[Sequence]):
-        bm = self.scheduler.block_manager
-        bs = bm.block_size
-        for seq in seqs:
-            if not seq.is_partial_recompute:
-                continue
-            entry = bm.get_image_kv_entry(seq.image_hashes[0])
-            if entry is None:
-                continue
-            img_start, img_end = seq.image_token_range
-            p = np.arange(img_start + seq.num_recompute_tokens, img_end, dtype=np.int64)
-            if p.size == 0:
-                continue
-            old_p = entry.img_start + (p - img_start)
-            ebt = np.asarray(entry.block_table, dtype=np.int64)
-            sbt = np.asarray(seq.block_table, dtype=np.int64)
-            old = ebt[old_p // bs] * bs + old_p % bs
-            new = sbt[p // bs] * bs + p % bs
-            deltas = None
-            if entry.rope_start is not None and seq.image_rope_start is not None:
-                deltas = [[a - b for a, b in zip(seq.image_rope_start, entry.rope_start)]]
-            self.model_runner.call("copy_image_kv", old, new, deltas)
+        plan = image_kv_copy_plan(seqs, self.scheduler.block_manager)
+        if plan is not None:
+            self.model_runner.call("copy_image_kv", *plan)
 
     def _store_image_kv(self, seqs: list[Sequence]):
         bm = self.scheduler.block_manager

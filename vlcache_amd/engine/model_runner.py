@@ -151,12 +151,13 @@ class ModelRunner:
                     mm["image_hashes"].append(seq.image_hashes[i])
                     mm["image_grid_thw"].append(tuple(int(x) for x in grids[i]))
                     mm["image_embeds"].append(None if embeds is None else embeds[i])
-                    mm["recompute"].append(seq.num_recompute_tokens if seq.is_partial_recompute else 0)
+                    r = seq.image_recompute[i] if seq.is_partial_recompute and i < len(seq.image_recompute) else None
+                    mm["recompute"].append(r if r is not None else 0)
             if seq.is_partial_recompute:
                 has_partial = True
-                a, e = seq.image_token_range
-                R = seq.num_recompute_tokens
-                runs = [(0, a + R), (e, n)]  # (sub1: Q = K = [0, a+R)), (sub2: Q = [e, n), K = [0, n))
+                # One image: (sub1: Q = K = [0, a+R)), (sub2: Q = [e, n), K = [0, n)); several
+                # images: every maximal run of computed tokens, K = everything before its end.
+                runs = seq.computed_runs()
                 for qs, qe in runs:
                     input_ids.append(ids[qs:qe])
                     positions.append(self._positions(seq, qs, qe))
@@ -165,8 +166,8 @@ class ModelRunner:
                     cu_k.append(cu_k[-1] + qe)
                     max_q, max_k = max(max_q, qe - qs), max(max_k, qe)
                     vbts.append(seq.block_table)
-                logit_indices.append(vidx + 1)
-                vidx += 2
+                logit_indices.append(vidx + len(runs) - 1)
+                vidx += len(runs)
             else:
                 input_ids.append(ids)
                 positions.append(self._positions(seq, 0, n))

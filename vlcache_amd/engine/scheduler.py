@@ -38,8 +38,7 @@ class Scheduler:
             seq = self.waiting[0]
             self.block_manager.try_partial_recompute(seq, self.image_token_id)
             if seq.is_partial_recompute:
-                img_start, img_end = seq.image_token_range
-                token_cost = len(seq) - ((img_end - img_start) - seq.num_recompute_tokens)
+                token_cost = len(seq) - seq.num_reused_tokens  # reused image tokens cost nothing
             else:
                 token_cost = len(seq)
             if num_batched_tokens + token_cost > self.max_num_batched_tokens or not self.block_manager.can_allocate(seq):
