@@ -400,10 +400,11 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 q/k/v and cached KV)",
         "config": {
-            "workload": f"{wl.name}: Qwen2.5-VL-3B shapes, {wl.model.num_layers} layers, heads "
+            "workload": f"{wl.name}: {wl.model.name} shapes, {wl.model.num_layers} layers, heads "
                         f"{wl.model.num_heads}/{wl.model.num_kv_heads}x{wl.model.head_dim}, "
-                        f"{wl.requests[0].prefix}+{wl.requests[0].n_image}+{wl.requests[0].suffix} tokens, "
-                        f"ratio {wl.requests[0].ratio}, paged blocks of 256",
+                        f"{len(wl.requests)} x ("
+                        + "+".join(str(v if k == 'text' else v[0] * v[1]) for k, v in wl.requests[0].parts())
+                        + f") tokens, ratio {wl.requests[0].ratio}, paged blocks of 256",
             "recomputed_tokens": hp.n_computed,
             "reused_tokens": hp.n_reused,
             "cu_seqlens_q": hp.cu_q_host,

@@ -43,17 +43,23 @@ class WarmPrefillHotPath:
         dev = self.device
         rng = np.random.default_rng(seed)
         reqs = wl.requests
-        img_len = reqs[0].n_image
         cached_prefix = reqs[0].cached_prefix
-        # block pool: one cached-image entry (shared) + each request's own blocks
-        entry_len = cached_prefix + img_len
-        entry_nb = -(-entry_len // BLOCK_SIZE)
+        # Block pool: one cached entry per distinct image (by its grid), stored standalone
+        # after cached_prefix text tokens, plus each request's own blocks.
+        grids = []
+        for r in reqs:
+            for _, _, hw in r.images():
+                if hw not in grids:
+                    grids.append(hw)
+        entry_nbs = [-(-(cached_prefix + hw[0] * hw[1]) // BLOCK_SIZE) for hw in grids]
         seq_nbs = [-(-r.length // BLOCK_SIZE) for r in reqs]
-        nb = entry_nb + sum(seq_nbs)
+        nb = sum(entry_nbs) + sum(seq_nbs)
         perm = rng.permutation(nb)
-        entry_bt = perm[:entry_nb]
+        entry_bts, p = {}, 0
+        for hw, n in zip(grids, entry_nbs):
+            entry_bts[hw] = perm[p:p + n]
+            p += n
         seq_bts = []
-        p = entry_nb
         for n in seq_nbs:
             seq_bts.append(perm[p:p + n])
             p += n
@@ -67,24 +73,26 @@ class WarmPrefillHotPath:
         self.k_caches = [self.kv_cache[0, l] for l in range(L)]
         self.v_caches = [self.kv_cache[1, l] for l in range(L)]
 
-        # reuse copy: old -> new slots per request, one rotation segment per request
+        # reuse copy: old -> new slots of every reused image token; one rotation segment
+        # per (request, image), shifted by the image's new rotary start minus its cached one
         old, new, seg, deltas = [], [], [], []
         slot_map, bts, cu_q, cu_k, pos_cols = [], [], [0], [0], []
-        for i, (r, bt) in enumerate(zip(reqs, seq_bts)):
-            img_s, img_e = r.prefix, r.prefix + r.n_image
-            reuse = np.arange(img_s + r.R, img_e) if r.ratio > 0 else np.arange(0)
-            old.append(_slots(entry_bt, cached_prefix + (reuse - img_s)))
-            new.append(_slots(bt, reuse))
-            seg.append(np.full(reuse.size, i, dtype=np.int32))
-            deltas.append([r.delta] * 3)
+        for r, bt in zip(reqs, seq_bts):
             if r.ratio > 0:
-                comp = np.concatenate([np.arange(0, img_s + r.R), np.arange(img_e, r.length)])
-            else:
-                comp = np.arange(r.length)
+                for (s_, e_, hw), rc, d in zip(r.images(), r.recompute(), r.deltas()):
+                    reuse = np.arange(s_ + rc, e_)
+                    old.append(_slots(entry_bts[hw], cached_prefix + (reuse - s_)))
+                    new.append(_slots(bt, reuse))
+                    seg.append(np.full(reuse.size, len(deltas), dtype=np.int32))
+                    deltas.append([d] * 3)
+            comp = np.concatenate([np.arange(a, b) for a, b in r.runs()])
             slot_map.append(_slots(bt, comp))
             toks = np.ones(r.length, dtype=np.int64)
-            toks[img_s:img_e] = IMAGE_TOKEN_ID
-            pos_all, _, _ = mrope_positions(toks, [(1, 2 * r.grid_hw[0], 2 * r.grid_hw[1])], IMAGE_TOKEN_ID)
+            grids_thw = []
+            for s_, e_, hw in r.images():
+                toks[s_:e_] = IMAGE_TOKEN_ID
+                grids_thw.append((1, 2 * hw[0], 2 * hw[1]))
+            pos_all, _, _ = mrope_positions(toks, grids_thw, IMAGE_TOKEN_ID)
             pos_cols.append(pos_all[:, comp])
             row = np.full(max(seq_nbs), -1, dtype=np.int32)
             row[:len(bt)] = bt
@@ -92,9 +100,13 @@ class WarmPrefillHotPath:
                 cu_q.append(cu_q[-1] + sq)
                 cu_k.append(cu_k[-1] + sk)
                 bts.append(row)
-        self.old_slots = torch.from_numpy(np.concatenate(old)).to(dev)
-        self.new_slots = torch.from_numpy(np.concatenate(new)).to(dev)
-        self.seg = torch.from_numpy(np.concatenate(seg)).to(dev)
+        if not deltas:
+            deltas = [[0, 0, 0]]
+        cat = lambda xs, dt: np.concatenate(xs).astype(dt) if xs else np.zeros(0, dtype=dt)
+        self.old_slots = torch.from_numpy(cat(old, np.int64)).to(dev)
+        self.new_slots = torch.from_numpy(cat(new, np.int64)).to(dev)
+        self.seg = torch.from_numpy(cat(seg, np.int32)).to(dev)
+        self.deltas = deltas
         self.cos_sin = kernels.rerotation_table(deltas, hd, m.rope_theta, m.mrope_section, device=dev)
         self.rotate = rotate
         self.n_reused = int(self.old_slots.numel())

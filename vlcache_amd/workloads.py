@@ -49,39 +49,90 @@ def merged_grid(width: int, height: int, patch: int = 14, merge: int = 2, min_pi
 
 @dataclass
 class WarmRequest:
-    prefix: int
-    n_image: int
-    suffix: int
-    ratio: float
-    cached_prefix: int  # text prefix length the image KV was cached at
+    """One warm request.  Single image: prefix text, an image of n_image tokens (merged
+    grid grid_hw), suffix text.  Several images: `layout`, a tuple of ("text", n) and
+    ("image", (h, w)) parts.  Every image was cached standalone after cached_prefix
+    text tokens; each keeps its first ceil(ratio * N) tokens recomputed."""
+    prefix: int = 0
+    n_image: int = 0
+    suffix: int = 0
+    ratio: float = 0.0
+    cached_prefix: int = 0  # text prefix length the image KV was cached at
     grid_hw: tuple = (0, 0)
+    layout: tuple | None = None
+
+    def parts(self):
+        if self.layout is not None:
+            return list(self.layout)
+        parts = [("text", self.prefix), ("image", tuple(self.grid_hw)), ("text", self.suffix)]
+        return [p for p in parts if p[0] == "image" or p[1] > 0]
+
+    def images(self):
+        """[(start, end, (h, w))] token range of each image."""
+        out, p = [], 0
+        for kind, val in self.parts():
+            n = val if kind == "text" else int(val[0]) * int(val[1])
+            if kind == "image":
+                out.append((p, p + n, (int(val[0]), int(val[1]))))
+            p += n
+        return out
+
+    def rope_starts(self):
+        """M-RoPE start position of each image: text advances 1 per token, an image max(h, w)."""
+        out, cur = [], 0
+        for kind, val in self.parts():
+            if kind == "text":
+                cur += val
+            else:
+                out.append(cur)
+                cur += max(int(val[0]), int(val[1]))
+        return out
+
+    def recompute(self):
+        """Recomputed tokens of each image: ceil(ratio * N) (IEEE double), all of it at ratio 0."""
+        return [math.ceil(self.ratio * (e - s)) if self.ratio > 0 else e - s for s, e, _ in self.images()]
 
     @property
     def R(self) -> int:
-        return math.ceil(self.ratio * self.n_image)
+        return self.recompute()[0]
 
     @property
     def length(self) -> int:
-        return self.prefix + self.n_image + self.suffix
+        return sum(v if k == "text" else int(v[0]) * int(v[1]) for k, v in self.parts())
 
     @property
     def n_reused(self) -> int:
-        return self.n_image - self.R
+        return sum((e - s) - r for (s, e, _), r in zip(self.images(), self.recompute()))
 
     @property
     def n_computed(self) -> int:
-        return self.prefix + self.R + self.suffix
+        return self.length - self.n_reused
+
+    def runs(self):
+        """Maximal runs [a, b) of computed tokens (one image: [0, P + R) and [P + N, len))."""
+        if self.ratio <= 0:
+            return [(0, self.length)]
+        runs, p = [], 0
+        for (s, e, _), r in zip(self.images(), self.recompute()):
+            if s + r < e:
+                if s + r > p:
+                    runs.append((p, s + r))
+                p = e
+        if p < self.length:
+            runs.append((p, self.length))
+        return runs
 
     def subseqs(self):
-        """[(sq, sk)] of the two virtual sub-sequences (ratio > 0) or of the full sequence."""
-        if self.ratio <= 0:
-            return [(self.length, self.length)]
-        a = self.prefix + self.R
-        return [(a, a), (self.suffix, self.length)]
+        """[(sq, sk)] of the virtual sub-sequences: queries [a, b), keys [0, b)."""
+        return [(b - a, b) for a, b in self.runs()]
+
+    def deltas(self):
+        """Rotary shift of each image: its start here minus its start when cached."""
+        return [st - self.cached_prefix for st in self.rope_starts()]
 
     @property
     def delta(self) -> int:
-        return self.prefix - self.cached_prefix
+        return self.deltas()[0]
 
 
 @dataclass
@@ -126,6 +177,18 @@ def cfg4(seed: int = 0) -> Workload:
     suf = rng.integers(16, 257, size=8)
     reqs = [WarmRequest(int(p), h * w, int(s), 0.05, 128, (h, w)) for p, s in zip(pre, suf)]
     return Workload("cfg4-3B-8seq-shared-4k-image-r0.05", QWEN25_VL_3B, reqs)
+
+
+def cfg5(num_layers: int = 28) -> Workload:
+    """7B, batch 4, two images per request: 64 text + 1920x1080 image (39x69 = 2691) + 64 text
+    + 4K image (77x137 = 10549) + 64 text = 13432 tokens, ratio 0.02, each image cached
+    standalone after 64 text tokens (image 1 keeps its rotary start, image 2 moves by 133)."""
+    g1, g2 = merged_grid(1920, 1080), merged_grid(3840, 2160)
+    layout = (("text", 64), ("image", g1), ("text", 64), ("image", g2), ("text", 64))
+    m = QWEN25_VL_7B if num_layers == QWEN25_VL_7B.num_layers else ModelShape(
+        f"Qwen2.5-VL-7B ({num_layers} layers)", num_layers, 28, 4, 128, 3584)
+    reqs = [WarmRequest(ratio=0.02, cached_prefix=64, layout=layout) for _ in range(4)]
+    return Workload("cfg5-7B-4seq-two-images-r0.02", m, reqs)
 
 
 def attention_flops(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, head_dim: int, causal: bool = True) -> int:
