@@ -96,9 +96,11 @@ __device__ __forceinline__ uint32_t lds_u32(const void* ptr) {
 // clobber keeps every LDS read of the buffer it overwrites (issued earlier in program
 // order) ahead of it.
 __device__ __forceinline__ void dma16_addr(const void* addr, uint32_t lds) {
+  // lds is uniform (wave and stage); readfirstlane keeps it in a scalar register
+  // where the compiler's divergence analysis cannot tell.
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :
-               : "s"(lds), "v"(addr)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(addr)
                : "m0", "memory");
 }
 
@@ -160,6 +162,29 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
 #undef VLC_WAIT_CASE
 }
 
+// 16- and 8-byte accesses at agent scope (sc1: written through to, and read from,
+// the level that is coherent across XCDs).  The 16-byte ones are inline assembly
+// (the compiler's atomics stop at 8 bytes); the compiler does not count those
+// loads in its waits, so their results are used only after an explicit vmcnt(0)
+// that takes them as operands.
+__device__ __forceinline__ void st16_agent(void* addr, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ f32x4 ld16_agent(const void* addr) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ void st_ml_agent(float* addr, float m, float l) {
+  const uint64_t bits = (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(l) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(addr), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_ml_agent(const float* addr) {
+  const uint64_t bits =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(addr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+}
+
 __device__ __forceinline__ float merge_weight(float m, float mx) {
   return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
 }
@@ -185,24 +210,17 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
   const int c = lane & 15;   // column (q head within the group)
   const int q4 = lane >> 4;  // 16-lane group
 
-  int ctx = p.seqlens[b];
-  ctx = max(0, min(ctx, p.max_keys));
-  const int n_splits = max(1, (ctx + p.key_chunk - 1) / p.key_chunk);
-  if (split >= n_splits) return;  // uniform over the workgroup, before any barrier
-  const int kb = split * p.key_chunk;
-  const int ke = min(ctx, kb + p.key_chunk);
+  // The wave's page ids and q fragments do not depend on the context length, so
+  // they are loaded before it (in bounds whatever it is): the three loads overlap
+  // instead of the page ids waiting for the length.
   const int wchunk = p.key_chunk / W;
-  const int wkb = kb + wave * wchunk;
-  const int wke = min(ke, wkb + wchunk);
-  const int n_tiles = wke > wkb ? (wke - wkb + kTileKeys - 1) / kTileKeys : 0;
-
+  const int64_t wkb64 = (int64_t)split * p.key_chunk + (int64_t)wave * wchunk;
   // Block ids of the wave's pages: lane i holds the id of page first_page + i.
-  const int first_page = wkb / p.page_size;
+  const int64_t first_page64 = wkb64 / p.page_size;
   int blk_reg = -1;
   {
-    const int pg = first_page + lane;
-    if (n_tiles > 0 && pg < p.bt_cols && lane < kMaxPagesPerWave)
-      blk_reg = p.block_table[(int64_t)b * p.bt_row_stride + pg];
+    const int64_t pg = first_page64 + lane;
+    if (pg < p.bt_cols && lane < kMaxPagesPerWave) blk_reg = p.block_table[(int64_t)b * p.bt_row_stride + pg];
   }
 
   // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[head c][32 kk + 8 q4 .. + 8].
@@ -218,6 +236,17 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
       qf[kk] = __builtin_bit_cast(bf16x8, w);
     }
   }
+
+  int ctx = p.seqlens[b];
+  ctx = max(0, min(ctx, p.max_keys));
+  const int n_splits = max(1, (ctx + p.key_chunk - 1) / p.key_chunk);
+  if (split >= n_splits) return;  // uniform over the workgroup, before any barrier
+  const int kb = split * p.key_chunk;
+  const int ke = min(ctx, kb + p.key_chunk);
+  const int wkb = kb + wave * wchunk;
+  const int wke = min(ke, wkb + wchunk);
+  const int n_tiles = wke > wkb ? (wke - wkb + kTileKeys - 1) / kTileKeys : 0;
+  const int first_page = wkb / p.page_size;
 
   uint8_t* wbuf = lds + wave * kWaveLds;
   const char* kbase = reinterpret_cast<const char*>(p.k + (int64_t)g * kHeadDim);
@@ -420,15 +449,10 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
     for (int pc = 0; pc < kPieces; ++pc) {
       const int d0 = ((tid >> 4) + pc * (W * 4)) * 8;
       float* po = p.part_o + ((pair * grid_splits + split) * grp + c2) * kHeadDim + d0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        __hip_atomic_store(po + i, acc[pc][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      st16_agent(po, f32x4{acc[pc][0], acc[pc][1], acc[pc][2], acc[pc][3]});
+      st16_agent(po + 4, f32x4{acc[pc][4], acc[pc][5], acc[pc][6], acc[pc][7]});
     }
-    if ((tid >> 4) == 0) {
-      float* pm = p.part_ml + ((pair * grid_splits + split) * grp + c2) * 2;
-      __hip_atomic_store(pm, mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(pm + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if ((tid >> 4) == 0) st_ml_agent(p.part_ml + ((pair * grid_splits + split) * grp + c2) * 2, mmax, lsum);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials have landed
   __syncthreads();
@@ -440,26 +464,29 @@ __global__ __launch_bounds__(W * 64) void decode_attn_kernel(const Params p) {
 
   // Online merge over the chunks, kMergeBatch chunks of loads in flight at a time;
   // thread (col, 4 dims) over the group's columns.
-  auto ld = [](const float* a) __attribute__((always_inline)) {
-    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
   constexpr int kMergeBatch = 16;
   for (int idx = tid; idx < grp * (kHeadDim / 4); idx += kThreads) {
     const int col = idx / (kHeadDim / 4);
     const int dd = (idx - col * (kHeadDim / 4)) * 4;
     float run_m = -INFINITY, run_l = 0.0f, tot[4] = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
-      float ms[kMergeBatch], ls[kMergeBatch], a[kMergeBatch][4];
+      float ms[kMergeBatch], ls[kMergeBatch];
+      f32x4 a[kMergeBatch];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         const int sx = min(s0 + u, n_splits - 1);  // clamped: extra slots get weight 0 below
-        const float* pm = p.part_ml + ((pair * grid_splits + sx) * grp + col) * 2;
-        const float* po = p.part_o + ((pair * grid_splits + sx) * grp + col) * kHeadDim + dd;
-        ms[u] = ld(pm);
-        ls[u] = ld(pm + 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[u][i] = ld(po + i);
+        a[u] = ld16_agent(p.part_o + ((pair * grid_splits + sx) * grp + col) * kHeadDim + dd);
+        const float2 ml = ld_ml_agent(p.part_ml + ((pair * grid_splits + sx) * grp + col) * 2);
+        ms[u] = ml.x;
+        ls[u] = ml.y;
       }
+      static_assert(kMergeBatch == 16, "one wait covers the batch");
+      asm volatile("s_waitcnt vmcnt(0)"
+                   : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
+                     "+v"(a[7]), "+v"(a[8]), "+v"(a[9]), "+v"(a[10]), "+v"(a[11]), "+v"(a[12]), "+v"(a[13]),
+                     "+v"(a[14]), "+v"(a[15])
+                   :
+                   : "memory");
       float bm = run_m;
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u)
