@@ -17,8 +17,10 @@ events on the launch stream around each attention call: main kernel + split-KV
 combine).  The fused RoPE + store time comes from the same events; the
 unfused sequence it replaces (torch eager RoPE, then the separate scatter) is
 timed after the step loop for comparison.  The rerotate is
-timed cold as well (a 512 MiB write evicts the MALL before each of 10 runs,
-median), next to a plain device copy of the same bytes timed the same way.
+timed cold as well (a 512 MiB read before each of 10 runs leaves the MALL
+holding clean lines of other data; median), next to a plain device copy of the
+same bytes timed the same way; both are also reported after a 512 MiB write,
+which leaves the MALL full of dirty lines whose write-backs compete.
 The paged decode attention of the batched 7B tail (batch 4, ~13.4k context) is
 timed cold on its own (kernels.decode).
 """
@@ -155,20 +157,24 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
     tr_ms = _mean_ms(ev_tr)
     rr_ms = _mean_ms(ev_rr) if hp.n_reused else None
     rr_in_step_ms = rr_ms
-    copy_ms = None
+    copy_ms = rr_dirty_ms = copy_dirty_ms = None
     if hp.n_reused:
-        # Bandwidth kernels are timed cold: a 512 MiB write evicts the 256 MB MALL
-        # before each run (median of 10).  A plain device copy of the same bytes,
-        # timed the same way, gives this box's practical copy ceiling.
+        # Bandwidth kernels are timed cold: a 512 MiB read evicts the 256 MB MALL
+        # before each run (median of 10), leaving it clean; a 512 MiB write instead
+        # leaves it dirty, and that variant is reported too.  A plain device copy
+        # of the same bytes, timed the same way, gives this box's copy rate.
         flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
         nbytes = workloads.rerotate_bytes(hp.n_reused, L, m.num_kv_heads, m.head_dim, with_v=True) // 2
         src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
 
-        def cold_ms(fn, reps=10):
+        def cold_ms(fn, reps=10, dirty=False):
             ts = []
             for _ in range(reps):
-                flush.fill_(1)
+                if dirty:
+                    flush.fill_(1)
+                else:
+                    flush.view(torch.int64).sum()
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record()
                 fn()
@@ -180,6 +186,8 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
 
         rr_ms = cold_ms(hp.rerotate)
         copy_ms = cold_ms(lambda: dst.copy_(src))
+        rr_dirty_ms = cold_ms(hp.rerotate, dirty=True)
+        copy_dirty_ms = cold_ms(lambda: dst.copy_(src), dirty=True)
         del flush, src, dst
     at_tflops = flops / (at_ms * 1e-3) / 1e12
     sc_bytes = workloads.scatter_bytes(hp.n_computed, m.num_kv_heads, m.head_dim)
@@ -195,6 +203,8 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
         rr_us=rr_ms * 1e3 if rr_ms else None, rr_gbps=rr_gbps, rr_bytes=rr_bytes,
         rr_in_step_us=rr_in_step_ms * 1e3 if rr_in_step_ms else None,
         copy_gbps=rr_bytes / (copy_ms * 1e-3) / 1e9 if copy_ms else None,
+        rr_dirty_us=rr_dirty_ms * 1e3 if rr_dirty_ms else None,
+        copy_dirty_gbps=rr_bytes / (copy_dirty_ms * 1e-3) / 1e9 if copy_dirty_ms else None,
         plan=(hp.plan.num_items, hp.plan.num_combine),
     )
 
@@ -435,9 +445,13 @@ def main():
             "rerotate": None if r["rr_us"] is None else {
                 "us_all_layers": round(r["rr_us"], 2), "bytes": r["rr_bytes"], "gbps": round(r["rr_gbps"], 1),
                 "frac_hbm_peak": round(r["rr_gbps"] / HBM_PEAK_GBPS, 4),
-                "timing": "cold (512 MiB MALL flush before each run), median of 10",
+                "timing": "cold: 512 MiB read before each run (MALL holds clean lines), median of 10",
                 "us_in_step": round(r["rr_in_step_us"], 2),
-                "plain_copy_same_bytes_gbps": round(r["copy_gbps"], 1)},
+                "plain_copy_same_bytes_gbps": round(r["copy_gbps"], 1),
+                "dirty_mall": {"us_all_layers": round(r["rr_dirty_us"], 2),
+                               "gbps": round(r["rr_bytes"] / (r["rr_dirty_us"] * 1e-6) / 1e9, 1),
+                               "plain_copy_same_bytes_gbps": round(r["copy_dirty_gbps"], 1),
+                               "timing": "512 MiB write before each run (MALL full of dirty lines)"}},
         },
         "ms_per_step_graph": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
         "warm_ttft": ttft,
