@@ -24,15 +24,16 @@
 // [8j, 8j+8) and the partner 16 bytes [hd/2+8j, hd/2+8j+8).  A token owns
 // (Hq + Hkv [+ Hkv for v]) * hd/16 units, enumerated head by head, so the
 // hd/16 lanes of a head read and write its whole 2*hd-byte row with 16-byte
-// accesses.  Each lane handles kUPT units spaced by the grid so that several
-// loads are in flight before the first store.
+// accesses.  Each lane handles kUPT units spaced by the grid, all their loads
+// in flight before the first store; one unit per lane (the most workgroups)
+// measured fastest for the 1247-token warm step (4.5 us against 5.1 us with two).
 #include "common.h"
 
 namespace vlc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUPT = 2;  // units per thread
+constexpr int kUPT = 1;  // units per thread
 
 struct RopeArgs {
   const uint16_t* q;
