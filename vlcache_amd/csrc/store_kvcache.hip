@@ -16,7 +16,7 @@ namespace vlc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kVPT = 4;  // chunks per thread (unrolled by hand in the kernel)
+constexpr int kVPT = 1;  // chunks per thread
 
 __global__ __launch_bounds__(kThreads) void store_kvcache_vec16(
     const char* __restrict__ key, int64_t key_stride_b, const char* __restrict__ value,
@@ -45,15 +45,13 @@ __global__ __launch_bounds__(kThreads) void store_kvcache_vec16(
     return ch;
   };
   for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < total; u += stride * kVPT) {
-    // kVPT = 4 chunks: all loads are issued before the first store.
-    const Chunk c0 = fetch(u);
-    const Chunk c1 = fetch(u + stride);
-    const Chunk c2 = fetch(u + 2 * stride);
-    const Chunk c3 = fetch(u + 3 * stride);
-    if (c0.dst) *reinterpret_cast<u32x4*>(c0.dst) = c0.data;
-    if (c1.dst) *reinterpret_cast<u32x4*>(c1.dst) = c1.data;
-    if (c2.dst) *reinterpret_cast<u32x4*>(c2.dst) = c2.data;
-    if (c3.dst) *reinterpret_cast<u32x4*>(c3.dst) = c3.data;
+    // All kVPT loads are issued before the first store.
+    Chunk c[kVPT];
+#pragma unroll
+    for (int k = 0; k < kVPT; ++k) c[k] = fetch(u + k * stride);
+#pragma unroll
+    for (int k = 0; k < kVPT; ++k)
+      if (c[k].dst) *reinterpret_cast<u32x4*>(c[k].dst) = c[k].data;
   }
 }
 
