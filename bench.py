@@ -12,11 +12,13 @@ of the 36 layers the fused M-RoPE of the 1247 recomputed tokens' q and k with
 the store of their k and v into the paged cache, and the varlen paged GQA
 causal attention of those tokens against the 10741-token cache.
 
-value = attention microseconds per layer (mean over the timed steps, HIP
-events on the launch stream around each attention call: main kernel + split-KV
-combine).  The fused RoPE + store time comes from the same events; the
-unfused sequence it replaces (torch eager RoPE, then the separate scatter) is
-timed after the step loop for comparison.  The rerotate is
+value = attention microseconds per layer: the step's 36 attention calls (main
+kernel + split-KV combine each, with the launch gap between them) captured as
+one HIP graph and replayed once per timed step, HIP events around each replay,
+divided by 36.  That is the GPU's time; HIP events around each eager call
+(also reported) add the host's Python and launch time whenever the host falls
+behind the GPU.  The fused RoPE + store, the separate scatter and torch's eager
+RoPE (the unfused sequence the fused kernel replaces) are timed the same way.  The rerotate is
 timed cold as well (a 512 MiB read before each of 10 runs leaves the MALL
 holding clean lines of other data; median), next to a plain device copy of the
 same bytes timed the same way; both are also reported after a 512 MiB write,
@@ -78,6 +80,43 @@ def _events(n):
 
 def _mean_ms(evs):
     return sum(s.elapsed_time(e) for s, e in evs) / max(1, len(evs))
+
+
+def _graph_us_per_call(fn_layer, num_layers: int, steps: int):
+    """GPU time of one call of fn_layer(layer), averaged over the layers: the
+    num_layers calls are captured in one HIP graph, replayed `steps` times with
+    events around each replay.  Host time (the Python wrappers, event records) is
+    not in the figure; the launch gaps between the kernels are.  None if the
+    calls cannot be captured."""
+    try:
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            for layer in range(num_layers):
+                fn_layer(layer)
+        torch.cuda.current_stream().wait_stream(st)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for layer in range(num_layers):
+                fn_layer(layer)
+        g.replay()
+        torch.cuda.synchronize()
+        ev = _events(steps)
+        for a, b in ev:
+            a.record()
+            g.replay()
+            b.record()
+        torch.cuda.synchronize()
+        return _mean_ms(ev) * 1e3 / num_layers
+    except Exception as e:  # report, do not hide
+        print(f"graph timing unavailable: {e!r}", file=sys.stderr)
+        return None
+
+
+def _timing_note(r, name: str) -> str:
+    if r["graph_timed"][name]:
+        return "GPU time per call: the step's per-layer calls as one HIP graph, replayed once per timed step"
+    return "HIP events around each eager call (graph capture unavailable)"
 
 
 def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
@@ -149,12 +188,20 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
             ev_tr[i][1].record()
     torch.cuda.synchronize()
 
+    # Per-call GPU times without host time: each kernel's 36 per-layer calls as a graph.
+    at_graph_us = _graph_us_per_call(hp.attention, L, steps)
+    rs_graph_us = _graph_us_per_call(hp.rope_store, L, steps)
+    sc_graph_us = _graph_us_per_call(hp.scatter, L, steps)
+    tr_graph_us = _graph_us_per_call(lambda layer: hp.torch_rope(), L, steps)
+
     cu_q, cu_k = hp.cu_q_host, hp.cu_k_host
     flops = workloads.attention_flops(cu_q, cu_k, m.num_heads, m.head_dim)
-    at_ms = _mean_ms(ev_at)
-    rs_ms = _mean_ms(ev_rs)
-    sc_ms = _mean_ms(ev_sc)
-    tr_ms = _mean_ms(ev_tr)
+    at_eager_ms = _mean_ms(ev_at)
+    at_ms = at_graph_us * 1e-3 if at_graph_us else at_eager_ms
+    rs_eager_ms, sc_eager_ms, tr_eager_ms = _mean_ms(ev_rs), _mean_ms(ev_sc), _mean_ms(ev_tr)
+    rs_ms = rs_graph_us * 1e-3 if rs_graph_us else rs_eager_ms
+    sc_ms = sc_graph_us * 1e-3 if sc_graph_us else sc_eager_ms
+    tr_ms = tr_graph_us * 1e-3 if tr_graph_us else tr_eager_ms
     rr_ms = _mean_ms(ev_rr) if hp.n_reused else None
     rr_in_step_ms = rr_ms
     copy_ms = rr_dirty_ms = copy_dirty_ms = None
@@ -200,6 +247,10 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
         wl=wl, hp=hp, wall=wall, graph_ms=graph_ms, flops=flops,
         at_us=at_ms * 1e3, at_tflops=at_tflops, sc_us=sc_ms * 1e3, sc_gbps=sc_gbps, sc_bytes=sc_bytes,
         rs_us=rs_ms * 1e3, rs_gbps=rs_gbps, rs_bytes=rs_bytes, torch_rope_us=tr_ms * 1e3,
+        graph_timed={"attention": at_graph_us is not None, "rope_store": rs_graph_us is not None,
+                     "scatter": sc_graph_us is not None, "torch_rope": tr_graph_us is not None},
+        eager_us={"attention": at_eager_ms * 1e3, "rope_store": rs_eager_ms * 1e3,
+                  "scatter": sc_eager_ms * 1e3, "torch_rope": tr_eager_ms * 1e3},
         rr_us=rr_ms * 1e3 if rr_ms else None, rr_gbps=rr_gbps, rr_bytes=rr_bytes,
         rr_in_step_us=rr_in_step_ms * 1e3 if rr_in_step_ms else None,
         copy_gbps=rr_bytes / (copy_ms * 1e-3) / 1e9 if copy_ms else None,
@@ -432,15 +483,21 @@ def main():
         "kernels": {
             "attention": {"us_per_layer": round(r["at_us"], 3), "gflop_per_layer": round(r["flops"] / 1e9, 3),
                           "tflops": round(r["at_tflops"], 2), "frac_mfma_peak": round(frac, 4),
-                          "work_items": r["plan"][0], "split_combines": r["plan"][1]},
+                          "work_items": r["plan"][0], "split_combines": r["plan"][1],
+                          "timing": _timing_note(r, "attention"),
+                          "eager_event_us_per_layer": round(r["eager_us"]["attention"], 3)},
             "rope_store": {"us_per_layer": round(r["rs_us"], 3), "bytes": r["rs_bytes"],
                            "gbps": round(r["rs_gbps"], 1), "frac_hbm_peak": round(r["rs_gbps"] / HBM_PEAK_GBPS, 4),
                            "replaces_us_per_layer": round(r["torch_rope_us"] + r["sc_us"], 3),
-                           "replaces": "torch eager M-RoPE of q and k + store_kvcache scatter"},
+                           "replaces": "torch eager M-RoPE of q and k + store_kvcache scatter",
+                           "timing": _timing_note(r, "rope_store"),
+                           "eager_event_us_per_layer": round(r["eager_us"]["rope_store"], 3)},
             "scatter": {"us_per_layer": round(r["sc_us"], 3), "bytes": r["sc_bytes"],
                         "gbps": round(r["sc_gbps"], 1), "frac_hbm_peak": round(r["sc_gbps"] / HBM_PEAK_GBPS, 4),
-                        "timing": "reference-API store_kvcache, timed outside the step"},
-            "torch_rope": {"us_per_layer": round(r["torch_rope_us"], 3)},
+                        "timing": "reference-API store_kvcache, outside the step; " + _timing_note(r, "scatter"),
+                        "eager_event_us_per_layer": round(r["eager_us"]["scatter"], 3)},
+            "torch_rope": {"us_per_layer": round(r["torch_rope_us"], 3), "timing": _timing_note(r, "torch_rope"),
+                           "eager_event_us_per_layer": round(r["eager_us"]["torch_rope"], 3)},
             "decode": decode,
             "rerotate": None if r["rr_us"] is None else {
                 "us_all_layers": round(r["rr_us"], 2), "bytes": r["rr_bytes"], "gbps": round(r["rr_gbps"], 1),
