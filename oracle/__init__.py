@@ -1,7 +1,7 @@
 """CPU oracle of the warm partial-recompute prefill path -- TEST INFRASTRUCTURE.
 
 This package restates, on the CPU, what the reference computes on the path the
-HIP kernels replace.  It is the checker, never the product: only ``tests/``,
+HIP kernels replace.  It checks the product and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it, and nothing in ``vlcache_amd`` does.
 
