@@ -4,54 +4,37 @@
 // Semantics (bit copy): for token n with slot = slot_mapping[n] >= 0, K row n and
 // V row n (row_bytes each) go to row `slot` of k_cache / v_cache; slot < 0 skips.
 //
-// Layout of the work: one 16-byte chunk per lane.  A token owns 2*C chunks
-// (C = row_bytes/16 for K, then C for V), so for Qwen2.5-VL-3B (2 kv heads x 128
-// dims, 512 B per row) one wave64 moves exactly one token: lanes 0-31 carry K,
-// lanes 32-63 carry V, each half a fully coalesced 512-byte read and write.
-// Each thread handles VPT chunks strided by the grid so that several 16-byte
-// loads are in flight before the first store.
+// Layout of the work: a lane moves 16-byte chunk c of both the K row and the V
+// row of its token (one slot lookup, two loads in flight, then two stores).  A
+// token owns C = row_bytes/16 chunks, so for Qwen2.5-VL-3B (2 kv heads x 128 dims,
+// 512 B per row) 32 consecutive lanes read and write a whole K row and a whole V
+// row, fully coalesced.  Against one chunk of K or of V per lane this measured
+// 4.89 us against 5.72 us for the 22 MB of a 10741-token layer (2.2 us either
+// way for 1247 tokens, where the launch dominates).
 #include "common.h"
 
 namespace vlc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kVPT = 1;  // chunks per thread
 
 __global__ __launch_bounds__(kThreads) void store_kvcache_vec16(
     const char* __restrict__ key, int64_t key_stride_b, const char* __restrict__ value,
     int64_t value_stride_b, char* __restrict__ k_cache, char* __restrict__ v_cache,
     int64_t num_slots, const int32_t* __restrict__ slot_mapping, int64_t num_tokens,
     int chunks_per_row, int64_t row_bytes) {
-  const int64_t chunks_per_token = 2 * (int64_t)chunks_per_row;
-  const int64_t total = num_tokens * chunks_per_token;
+  const int64_t total = num_tokens * (int64_t)chunks_per_row;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
-  struct Chunk {
-    u32x4 data;
-    char* dst;  // nullptr = nothing to store
-  };
-  auto fetch = [&](int64_t w) -> Chunk {
-    Chunk ch{{0u, 0u, 0u, 0u}, nullptr};
-    if (w >= total) return ch;
-    const int64_t n = w / chunks_per_token;
-    const int c = (int)(w - n * chunks_per_token);
+  for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < total; u += stride) {
+    const uint32_t n = (uint32_t)u / (uint32_t)chunks_per_row;
+    const int cc = (int)((uint32_t)u - n * (uint32_t)chunks_per_row);
     const int32_t slot = slot_mapping[n];
-    if (slot < 0 || slot >= num_slots) return ch;
-    const bool is_v = c >= chunks_per_row;
-    const int cc = is_v ? c - chunks_per_row : c;
-    const char* src = is_v ? value + n * value_stride_b : key + n * key_stride_b;
-    ch.data = *reinterpret_cast<const u32x4*>(src + (int64_t)cc * 16);
-    ch.dst = (is_v ? v_cache : k_cache) + (int64_t)slot * row_bytes + (int64_t)cc * 16;
-    return ch;
-  };
-  for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < total; u += stride * kVPT) {
-    // All kVPT loads are issued before the first store.
-    Chunk c[kVPT];
-#pragma unroll
-    for (int k = 0; k < kVPT; ++k) c[k] = fetch(u + k * stride);
-#pragma unroll
-    for (int k = 0; k < kVPT; ++k)
-      if (c[k].dst) *reinterpret_cast<u32x4*>(c[k].dst) = c[k].data;
+    if (slot < 0 || slot >= num_slots) continue;
+    const u32x4 kd = *reinterpret_cast<const u32x4*>(key + (int64_t)n * key_stride_b + (int64_t)cc * 16);
+    const u32x4 vd = *reinterpret_cast<const u32x4*>(value + (int64_t)n * value_stride_b + (int64_t)cc * 16);
+    const int64_t o = (int64_t)slot * row_bytes + (int64_t)cc * 16;
+    *reinterpret_cast<u32x4*>(k_cache + o) = kd;
+    *reinterpret_cast<u32x4*>(v_cache + o) = vd;
   }
 }
 
@@ -98,8 +81,9 @@ VLC_API int vlc_store_kvcache(const void* key, int64_t key_row_stride, const voi
                    aligned16(value) && aligned16(k_cache) && aligned16(v_cache);
   if (vec) {
     const int cpr = (int)(row_bytes / 16);
-    const int64_t total = num_tokens * 2 * cpr;
-    int64_t blocks = (total + (int64_t)kThreads * kVPT - 1) / ((int64_t)kThreads * kVPT);
+    const int64_t total = num_tokens * cpr;
+    if (total >= ((int64_t)1 << 32)) return VLC_ERR_UNSUPPORTED;  // 32-bit chunk index
+    int64_t blocks = (total + kThreads - 1) / kThreads;
     if (blocks < 1) blocks = 1;
     if (blocks > (1 << 20)) blocks = 1 << 20;
     hipLaunchKernelGGL(store_kvcache_vec16, dim3((unsigned)blocks), dim3(kThreads), 0, s,
