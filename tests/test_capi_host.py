@@ -149,6 +149,34 @@ def test_kernel_wrappers_refuse_cpu_tensors(lib):
                                   torch.zeros(4, dtype=torch.int32))
 
 
+def test_copy_entry_points_validate_before_launching(lib):
+    """Argument errors come back as status codes before any launch: these calls pass
+    placeholder (aligned, never dereferenced) device addresses and run without a GPU."""
+    A = 1 << 20  # a 16-byte aligned placeholder address
+    # empty work is a no-op
+    assert lib.vlc_store_kvcache(A, 256, A, 256, A, A, 16, A, 0, 256, 2, None) == 0
+    assert lib.vlc_store_kvcache(A, 256, A, 256, A, A, 16, A, -1, 256, 2, None) == _lib.VLC_ERR_INVALID
+    # a row stride shorter than the row
+    assert lib.vlc_store_kvcache(A, 128, A, 256, A, A, 16, A, 4, 256, 2, None) == _lib.VLC_ERR_INVALID
+    # 2^28 tokens x 32 chunks of 16 bytes: beyond the kernel's 32-bit chunk index
+    assert lib.vlc_store_kvcache(A, 256, A, 256, A, A, 16, A, 1 << 28, 256, 2, None) == _lib.VLC_ERR_UNSUPPORTED
+    # re-rotation: 2^28 tokens x 16 units per token (2 kv heads x 128 dims) > 2^32 - 1
+    row = 2 * 128
+    slots = 1 << 29
+    layer_stride = slots * row
+    args = dict(plane_stride=36 * layer_stride, layer_stride=layer_stride, num_layers=36)
+    st = lib.vlc_rerotate_copy_kv(A, args["plane_stride"], args["layer_stride"], args["num_layers"], A, A,
+                                  1 << 28, slots, 2, 128, None, A, 1, 1, None)
+    assert st == _lib.VLC_ERR_UNSUPPORTED
+    st = lib.vlc_rerotate_copy_kv(A, args["plane_stride"], args["layer_stride"], args["num_layers"], A, A,
+                                  0, slots, 2, 128, None, A, 1, 1, None)
+    assert st == 0
+    # head_dim not a multiple of 16; a layer stride shorter than the slots it must hold
+    assert lib.vlc_rerotate_copy_kv(A, 0, 0, 1, A, A, 4, 16, 2, 120, None, A, 1, 1, None) == _lib.VLC_ERR_UNSUPPORTED
+    assert lib.vlc_rerotate_copy_kv(A, 2 * 16 * row, 16 * row - 8, 1, A, A, 4, 16, 2, 128, None, A, 1, 1,
+                                    None) == _lib.VLC_ERR_INVALID
+
+
 def test_workload_counts_match_hand_derivation():
     # unmasked (query, key) pairs x 4 * hd * Hq: cfg1 49,372 pairs; cfg2 1,385,744; cfg3 57,689,911
     for wl, pairs in ((workloads.cfg1(), 49372), (workloads.cfg2(), 1385744), (workloads.cfg3(), 57689911)):

@@ -56,7 +56,12 @@ SIGNATURES = {
 
 ABI_VERSION = 1
 
+VLC_OK = 0
+VLC_ERR_INVALID = -1
+VLC_ERR_UNSUPPORTED = -2
+VLC_ERR_WORKSPACE = -3
 VLC_ERR_CAPACITY = -4
+VLC_ERR_PLAN = -5
 
 
 class VLCError(RuntimeError):
