@@ -363,6 +363,29 @@ def test_attention_batched_ragged(dev):
     assert_close(out, ref, what="ragged attention")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_attention_random_shapes(dev, seed):
+    """Seeded random varlen problems: sequence count, lengths (empty and short ones
+    included), head layouts, page sizes, causal or not, and planner CU counts."""
+    r = np.random.default_rng(1000 + seed)
+    n = int(r.integers(1, 5))
+    subs = []
+    for _ in range(n):
+        sq = int(r.choice([0, 1, int(r.integers(2, 200))]))
+        sk = sq + int(r.integers(0, 1200)) if r.random() < 0.9 else max(0, sq - int(r.integers(1, 20)))
+        subs.append((sq, sk))
+    hq, hkv = [(16, 2), (28, 4), (8, 1), (32, 2), (12, 12)][int(r.integers(0, 5))]
+    page = int(r.choice([16, 64, 256]))
+    causal = bool(r.random() < 0.7)
+    num_cus = [None, 8, 300][int(r.integers(0, 3))]
+    say(f"attention random seed={seed}: subs={subs} heads={hq}/{hkv} page={page} causal={causal} "
+        f"num_cus={num_cus}")
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(300 + seed, hq, hkv, subs, page=page)
+    out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=causal, num_cus=num_cus)
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), page)
+    assert_close(out, ref, what=f"random attention seed {seed}")
+
+
 def test_attention_small_pages_and_non_causal(dev):
     say("attention: page size 16 (per-row lookup), causal and non-causal")
     subs = [(40, 100), (7, 7), (64, 64)]
