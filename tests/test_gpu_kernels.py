@@ -167,6 +167,36 @@ def test_rerotate_segments_negative_and_sectioned_deltas(dev):
     assert (out[0].view(torch.int16) != ref[0].view(torch.int16)).sum().item() == 0
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_rerotate_random_shapes(dev, seed):
+    """Seeded random re-rotations: layers, kv heads, token counts, 1-3 segments with
+    random (dt, dh, dw) deltas, M-RoPE or 1-D sections; V and K bit for bit."""
+    r = np.random.default_rng(2000 + seed)
+    L, hkv = int(r.integers(1, 5)), int(r.choice([1, 2, 4]))
+    nb = 12
+    kv = _rerotate_setup(L, nb, seed=60 + seed, hkv=hkv)
+    n = int(r.integers(1, 6 * 256 // 2))
+    perm = r.permutation(nb * 256)
+    old, new = perm[:n].tolist(), perm[n:2 * n].tolist()
+    nseg = int(r.integers(1, 4))
+    seg = torch.from_numpy(r.integers(0, nseg, n).astype(np.int32))
+    deltas = r.integers(-300, 300, (nseg, 3)).tolist()
+    section = [16, 24, 24] if r.random() < 0.7 else None
+    if section is None:
+        deltas = [[d[0]] * 3 for d in deltas]
+    say(f"rerotate random seed={seed}: L={L} hkv={hkv} n={n} deltas={deltas} section={section}")
+    cs = orope.rerotation_cos_sin(deltas, 128, 1e6, section)
+    ref = kv.clone()
+    orope.rerotate_copy_kv(ref, old, new, cs, seg)
+    kv_d = kv.to(dev)
+    kernels.rerotate_copy_kv(kv_d, torch.tensor(old, device=dev), torch.tensor(new, device=dev), cs.to(dev),
+                             seg.to(dev))
+    torch.cuda.synchronize()
+    out = kv_d.cpu()
+    assert torch.equal(out[1].view(torch.int16), ref[1].view(torch.int16)), "V"
+    assert torch.equal(out[0].view(torch.int16), ref[0].view(torch.int16)), "K"
+
+
 # ----------------------------------------------------------------------------- fused RoPE + scatter
 def _recomputed_mrope_positions():
     """M-RoPE positions of the 1247 recomputed tokens of the 4K-image request (ratio 0.1)."""
@@ -509,6 +539,20 @@ def test_decode_3b_ragged_lengths_and_empty(dev):
     lens = [0, 1, 31, 32, 33, 700, 10741]
     outs, _ = _decode_case(dev, lens, 16, 2, seed=61)
     assert torch.count_nonzero(outs[0][0]) == 0  # no key: zeros
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_decode_random_shapes(dev, seed):
+    """Seeded random decode batches: batch size, context lengths (1 token to 5000), head
+    layouts, page sizes and forced split counts."""
+    r = np.random.default_rng(3000 + seed)
+    B = int(r.integers(1, 7))
+    lens = [int(x) for x in r.integers(1, 5000, B)]
+    hq, hkv = [(16, 2), (28, 4), (8, 1), (32, 2), (12, 12)][int(r.integers(0, 5))]
+    page = int(r.choice([16, 64, 256]))
+    splits = [0, 1, int(r.integers(2, 40))][int(r.integers(0, 3))]
+    say(f"decode random seed={seed}: lens={lens} heads={hq}/{hkv} page={page} splits={splits}")
+    _decode_case(dev, lens, hq, hkv, seed=400 + seed, page=page, num_splits=splits)
 
 
 @pytest.mark.parametrize("splits", [1, 3, 32])
