@@ -82,6 +82,21 @@ def test_scatter_out_of_range_slot_skipped(dev):
     assert torch.equal(kc_d.cpu().view(-1, hkv, hd), ref)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_scatter_random_shapes(dev, seed):
+    """Seeded random scatters: token counts, kv heads, head dims, strided V rows, skip rates,
+    bf16 and fp32 rows; bit for bit."""
+    r = np.random.default_rng(4000 + seed)
+    hkv, hd = int(r.choice([1, 2, 4, 8])), int(r.choice([64, 128]))
+    n = int(r.integers(1, 3000))
+    nb, bs = int(r.integers(-(-n // 256) + 1, 40)), 256
+    dtype = torch.bfloat16 if r.random() < 0.75 else torch.float32
+    v_row = None if r.random() < 0.5 else hkv * hd * 3
+    neg = int(r.choice([0, 3, 11]))
+    say(f"scatter random seed={seed}: n={n} hkv={hkv} hd={hd} blocks={nb} dtype={dtype} v_row={v_row} neg_every={neg}")
+    _scatter_case(dev, n, hkv, hd, nb, bs, seed=500 + seed, dtype=dtype, neg_every=neg, v_row=v_row)
+
+
 # ----------------------------------------------------------------------------- rerotate
 def _rerotate_setup(L, nb, seed, hkv=2, hd=128):
     g = gen(seed)
@@ -255,6 +270,25 @@ def _rope_case(dev, positions, hq, hkv, section, seed, nb=8, bs=256, neg_every=5
     if store:
         assert np.array_equal(bits(kc_d), bits(kc_ref)), "k_cache"
         assert np.array_equal(bits(vc_d), bits(vc_ref)), "v_cache"
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_rope_store_random_shapes(dev, seed):
+    """Seeded random fused RoPE + store calls: token counts, head layouts, 1-D or M-RoPE
+    positions with random sections, skipped slots, q in place or not, k_out or not."""
+    r = np.random.default_rng(5000 + seed)
+    n = int(r.integers(1, 2500))
+    hq, hkv = [(16, 2), (28, 4), (8, 1), (32, 2), (12, 12)][int(r.integers(0, 5))]
+    if r.random() < 0.6:
+        cut = sorted(r.choice(np.arange(1, 64), 2, replace=False).tolist())
+        section = [cut[0], cut[1] - cut[0], 64 - cut[1]]
+        pos = r.integers(0, 16000, (3, n))
+    else:
+        section, pos = None, r.integers(0, 16000, n)
+    nb = -(-n // 256) + 2
+    kw = dict(in_place=bool(r.random() < 0.5), want_k=bool(r.random() < 0.5), neg_every=int(r.choice([0, 5])))
+    say(f"rope_store random seed={seed}: n={n} heads={hq}/{hkv} section={section} {kw}")
+    _rope_case(dev, pos, hq, hkv, section, seed=600 + seed, nb=nb, **kw)
 
 
 def test_rope_store_4k_image_recomputed_mrope(dev):
