@@ -47,10 +47,16 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale: float, 
         qb = q[cu_q[b]:cu_q[b + 1]].float().transpose(0, 1)      # [Hq, sq, hd]
         for a in range(0, sq, q_chunk):
             e = min(sq, a + q_chunk)
+            # Keys past the chunk's last causal limit are masked for every row of the
+            # chunk; leaving them out of the product changes no result.
+            hi = min(sk, max(0, e + sk - sq)) if causal else sk
+            if hi == 0:
+                continue
             i = torch.arange(a, e)[:, None]
-            j = torch.arange(sk)[None, :]
-            mask = (j <= i + sk - sq) if causal else torch.ones(e - a, sk, dtype=torch.bool)
-            o = F.scaled_dot_product_attention(qb[:, a:e], kb, vb, attn_mask=mask, scale=softmax_scale)
+            j = torch.arange(hi)[None, :]
+            mask = (j <= i + sk - sq) if causal else torch.ones(e - a, hi, dtype=torch.bool)
+            o = F.scaled_dot_product_attention(qb[:, a:e], kb[:, :hi], vb[:, :hi], attn_mask=mask,
+                                               scale=softmax_scale)
             # flash-attn convention: a row with no visible key is 0 (SDPA gives NaN).
             o = torch.where(mask.any(dim=1)[None, :, None], o, torch.zeros_like(o))
             out[cu_q[b] + a:cu_q[b] + e] = o.transpose(0, 1)

@@ -19,7 +19,7 @@ import torch
 from oracle import attention as oattn
 from oracle import rope as orope
 from oracle import scatter as oscat
-from tests._util import assert_close, bits, gen, randn_bf16, say
+from tests._util import assert_attn_close, assert_close, bits, gen, randn_bf16, say
 from vlcache_amd import SamplingParams
 from vlcache_amd.layers.attention import Attention
 from vlcache_amd.utils.context import reset_context, set_context
@@ -61,7 +61,7 @@ def test_attention_layer_paged_prefill_through_context(dev):
                         slot_phys.numpy())
     assert np.array_equal(bits(attn.k_cache), bits(kref)) and np.array_equal(bits(attn.v_cache), bits(vref))
     ref = oattn.varlen_attention(q, kref, vref, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), page)
-    assert_close(out, ref, what="Attention paged prefill")
+    assert_attn_close(out, ref, what="Attention paged prefill")
 
 
 def test_attention_layer_decode(dev):
@@ -89,7 +89,7 @@ def test_attention_layer_decode(dev):
     kref.view(-1, hkv, 128)[slot.long()] = k1
     vref.view(-1, hkv, 128)[slot.long()] = v1
     ref = oattn.varlen_attention(q, kref, vref, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), page)
-    assert_close(out[:, 0], ref, what="Attention decode")
+    assert_attn_close(out[:, 0], ref, what="Attention decode")
 
 
 def _engine(ratio, blocks=64, seed=0):

@@ -14,7 +14,7 @@ import torch
 
 from oracle import attention as oattn
 from oracle import rope as orope
-from tests._util import assert_close, say
+from tests._util import assert_attn_close, say
 from vlcache_amd import workloads
 from vlcache_amd.hotpath import WarmPrefillHotPath
 
@@ -52,5 +52,5 @@ def test_two_image_batch_step_matches_oracle(dev):
     # attention of the last layer through the block tables
     o_ref = oattn.varlen_attention(q_ref, ref[0, 1], ref[1, 1], hp.cu_q_host, hp.cu_k_host, hp.scale, True,
                                    hp.block_tables.cpu().tolist(), 256)
-    assert_close(out, o_ref, what="two-image batch attention")
+    assert_attn_close(out, o_ref, what="two-image batch attention")
     assert np.isfinite(out.float().numpy()).all()

@@ -14,7 +14,7 @@ from oracle import attention as oattn
 from oracle import prefill as opre
 from oracle import rope as orope
 from oracle import scatter as oscat
-from tests._util import assert_close, bits, gen, randn_bf16, say
+from tests._util import assert_attn_close, assert_close, bits, gen, randn_bf16, say
 from vlcache_amd import kernels
 
 pytestmark = pytest.mark.gpu
@@ -385,7 +385,7 @@ def test_attention_cfg1_paged(dev, num_cus):
     out, plan = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, num_cus=num_cus)
     print(f"plan items={plan.num_items} combines={plan.num_combine}")
     ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
-    assert_close(out, ref, what="cfg1 attention")
+    assert_attn_close(out, ref, what="cfg1 attention")
 
 
 @pytest.mark.parametrize("subs,num_cus", [([(64, 10741), (300, 300)], 256), ([(16, 20000)], 4096)])
@@ -405,7 +405,7 @@ def test_attention_many_splits_repeat(dev, subs, num_cus):
     outs = [kernels.varlen_attention(*args, plan=plan).cpu() for _ in range(3)]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
-    assert_close(outs[0], ref, what="many-split attention")
+    assert_attn_close(outs[0], ref, what="many-split attention")
 
 
 def test_attention_7b_group7_multi_run(dev):
@@ -414,7 +414,7 @@ def test_attention_7b_group7_multi_run(dev):
     q, kc, vc, bt, cu_q, cu_k = _paged_case(21, hq, hkv, [(118, 118), (275, 3030), (64, 3200)])
     out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
     ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
-    assert_close(out, ref, what="7B attention")
+    assert_attn_close(out, ref, what="7B attention")
 
 
 def test_attention_batched_ragged(dev):
@@ -424,7 +424,7 @@ def test_attention_batched_ragged(dev):
     q, kc, vc, bt, cu_q, cu_k = _paged_case(22, hq, hkv, subs)
     out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
     ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
-    assert_close(out, ref, what="ragged attention")
+    assert_attn_close(out, ref, what="ragged attention")
 
 
 @pytest.mark.parametrize("seed", range(12))
@@ -447,7 +447,7 @@ def test_attention_random_shapes(dev, seed):
     q, kc, vc, bt, cu_q, cu_k = _paged_case(300 + seed, hq, hkv, subs, page=page)
     out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=causal, num_cus=num_cus)
     ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), page)
-    assert_close(out, ref, what=f"random attention seed {seed}")
+    assert_attn_close(out, ref, what=f"random attention seed {seed}")
 
 
 def test_attention_small_pages_and_non_causal(dev):
@@ -458,7 +458,7 @@ def test_attention_small_pages_and_non_causal(dev):
     for causal in (True, False):
         out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=causal)
         ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), 16)
-        assert_close(out, ref, what=f"page-16 causal={causal}")
+        assert_attn_close(out, ref, what=f"page-16 causal={causal}")
 
 
 def test_attention_rows_without_keys_are_zero(dev):
@@ -469,7 +469,7 @@ def test_attention_rows_without_keys_are_zero(dev):
     out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv)
     ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
     assert torch.count_nonzero(out[:30].float()) == 0
-    assert_close(out, ref, what="sk<sq")
+    assert_attn_close(out, ref, what="sk<sq")
 
 
 def test_attention_block_permutation_bit_identical(dev):
@@ -502,7 +502,7 @@ def test_attention_contiguous_dense_strided_v(dev):
     torch.cuda.synchronize()
     v = qkv[:, (hq + hkv) * 128:].reshape(n, hkv, 128)
     ref = oattn.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, True, None)
-    assert_close(out.cpu(), ref, what="dense contiguous")
+    assert_attn_close(out.cpu(), ref, what="dense contiguous")
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -525,7 +525,7 @@ def test_attention_score_gap_between_lane_halves(dev, causal):
     torch.cuda.synchronize()
     ref = oattn.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, causal, None)
     assert torch.isfinite(out.cpu().float()).all(), "non-finite output"
-    assert_close(out.cpu(), ref, what="score gap")
+    assert_attn_close(out.cpu(), ref, what="score gap")
 
 
 # ----------------------------------------------------------------------------- decode attention
@@ -558,7 +558,7 @@ def _decode_case(dev, lens, hq, hkv, seed, page=256, num_splits=0, extra_blocks=
         torch.cuda.synchronize()
         outs.append(o.cpu())
     for o in outs:
-        assert_close(o, ref, what=f"decode {lens} hq={hq} hkv={hkv} splits={num_splits}")
+        assert_attn_close(o, ref, what=f"decode {lens} hq={hq} hkv={hkv} splits={num_splits}")
     return outs, plan
 
 
@@ -620,7 +620,7 @@ def test_decode_score_gap_between_lane_groups(dev):
                                    device=dev), bt.to(dev), 128 ** -0.5, plan=plan)
     torch.cuda.synchronize()
     assert torch.isfinite(out.cpu().float()).all()
-    assert_close(out.cpu(), ref, what="decode score gap")
+    assert_attn_close(out.cpu(), ref, what="decode score gap")
 
 
 def test_decode_small_pages_group7(dev):

@@ -110,3 +110,44 @@ def test_copy_image_kv_gathers_before_writing():
     for o, nw in zip(old, new):
         assert (f1[:, :, nw] == f0[:, :, o]).all()
     assert (f1[:, :, [3, 4, 7]] == f0[:, :, [3, 4, 7]]).all()
+
+
+def test_per_row_bar_catches_a_dropped_split():
+    """A planted mistake on the CPU: one 8-position query tile of the 64 x 10741 suffix
+    loses one 384-key split (keys [384, 768) of its 8 q heads of kv head 0).  The global
+    bar (max-abs 2e-2, cosine 0.9995) passes it; the per-(row, head) bar must not."""
+    from tests._util import assert_close, assert_rows_close
+
+    g = torch.Generator().manual_seed(7)
+    sq, sk, hq, hkv = 64, 10741, 16, 2
+    q = torch.randn(sq + 300, hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(sk + 300, hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(sk + 300, hkv, 128, generator=g).to(torch.bfloat16)
+    cu_q, cu_k = [0, sq, sq + 300], [0, sk, sk + 300]
+    ref = oattn.varlen_attention(q, k, v, cu_q, cu_k, 128 ** -0.5, True, None)
+    bad = ref.clone()
+    rows = torch.arange(8, 16)
+    for h in range(8):  # q heads of kv head 0
+        qi = q[rows, h].float()
+        kk, vv = k[:sk, 0].float(), v[:sk, 0].float()
+        keep = torch.ones(rows.numel(), sk, dtype=torch.bool)
+        keep[:, 384:768] = False
+        keep &= torch.arange(sk)[None, :] <= rows[:, None] + sk - sq
+        bad[rows, h] = F.scaled_dot_product_attention(qi[None], kk[None], vv[None], attn_mask=keep[None],
+                                                      scale=128 ** -0.5)[0]
+    assert_close(bad, ref, what="planted dropped split (global bar)")
+    with pytest.raises(AssertionError, match="cosine"):
+        assert_rows_close(bad, ref, what="planted dropped split")
+    # and the bar passes what it should: the oracle against its own bf16 rounding
+    assert_rows_close(ref.to(torch.bfloat16), ref, what="bf16 rounding of the oracle")
+
+
+def test_per_row_bar_demands_zero_rows():
+    from tests._util import assert_rows_close
+
+    ref = torch.zeros(4, 2, 128)
+    ref[2:] = torch.randn(2, 2, 128)
+    out = ref.clone()
+    out[0, 1, 5] = 1e-3  # a row that sees no key must stay exactly zero
+    with pytest.raises(AssertionError, match="non-zero"):
+        assert_rows_close(out, ref)

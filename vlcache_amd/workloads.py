@@ -156,27 +156,34 @@ def cfg1() -> Workload:
     return Workload("cfg1-3B-1layer-1k-image-r0.1", m, [WarmRequest(64, 1024, 32, 0.1, 16, (32, 32))])
 
 
-def cfg2() -> Workload:
+def _shape_3b(num_layers: int) -> ModelShape:
+    if num_layers == QWEN25_VL_3B.num_layers:
+        return QWEN25_VL_3B
+    return ModelShape(f"Qwen2.5-VL-3B ({num_layers} layers)", num_layers, 16, 2, 128, 2048)
+
+
+def cfg2(num_layers: int = 36) -> Workload:
     """3B, 36 layers, 128 + 4K image (77x137 = 10549) + 64, ratio 0.1, cached at prefix 40."""
     h, w = merged_grid(3840, 2160)
-    return Workload("cfg2-3B-4k-image-r0.1", QWEN25_VL_3B, [WarmRequest(128, h * w, 64, 0.1, 40, (h, w))])
+    return Workload("cfg2-3B-4k-image-r0.1", _shape_3b(num_layers),
+                    [WarmRequest(128, h * w, 64, 0.1, 40, (h, w))])
 
 
-def cfg3() -> Workload:
+def cfg3(num_layers: int = 36) -> Workload:
     """3B, 4K image, ratio 0.0: dense causal prefill of the whole 10741-token sequence."""
     h, w = merged_grid(3840, 2160)
-    return Workload("cfg3-3B-4k-image-full-recompute", QWEN25_VL_3B,
+    return Workload("cfg3-3B-4k-image-full-recompute", _shape_3b(num_layers),
                     [WarmRequest(128, h * w, 64, 0.0, 128, (h, w))])
 
 
-def cfg4(seed: int = 0) -> Workload:
+def cfg4(seed: int = 0, num_layers: int = 36) -> Workload:
     """3B, 8 warm requests sharing one cached 4K image; prefixes U[16,512], suffixes U[16,256]."""
     h, w = merged_grid(3840, 2160)
     rng = np.random.default_rng(seed)
     pre = rng.integers(16, 513, size=8)
     suf = rng.integers(16, 257, size=8)
     reqs = [WarmRequest(int(p), h * w, int(s), 0.05, 128, (h, w)) for p, s in zip(pre, suf)]
-    return Workload("cfg4-3B-8seq-shared-4k-image-r0.05", QWEN25_VL_3B, reqs)
+    return Workload("cfg4-3B-8seq-shared-4k-image-r0.05", _shape_3b(num_layers), reqs)
 
 
 def cfg5(num_layers: int = 28) -> Workload:
