@@ -33,6 +33,7 @@ extern "C" {
 #define VLC_ERR_WORKSPACE (-3)   /* workspace smaller than the plan requires */
 #define VLC_ERR_CAPACITY (-4)    /* host plan buffer too small */
 #define VLC_ERR_PLAN (-5)        /* plan does not match the call's shapes */
+#define VLC_ERR_SCRATCH (-6)     /* the call needs more than the fixed scratch of a *_noalloc entry */
 
 const char* vlc_status_string(int status);
 int vlc_abi_version(void);
@@ -233,6 +234,33 @@ int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, co
                     int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
                     void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                     void* stream);
+
+/*
+ * Allocation-free variant of vlc_decode_attn.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory or pass a
+ * workspace -- code under HIP graph capture (the reference replays its decode
+ * step from a captured CUDA graph, engine/model_runner.py:418-432,453-479), tight serving
+ * loops, harnesses that forbid allocation.
+ *
+ * Arguments and results are those of vlc_decode_attn without workspace and
+ * workspace_bytes: the ticket counters and split partials live in a fixed
+ * device array inside the library, VLC_DECODE_NOALLOC_MAX_BYTES (16 MiB) per
+ * device, held until the process ends.  A call whose plan has grid_splits > 1
+ * and whose workspace (as vlc_decode_attn_plan sizes it) exceeds that returns
+ * VLC_ERR_SCRATCH before any device work; with grid_splits == 1 no scratch is
+ * used.  The first call on a device looks the array up and enqueues a small
+ * kernel on `stream` that zeroes its counters; no call allocates, frees or
+ * synchronises.  Every call on a device shares that device's array: calls that
+ * overlap on one device (other streams, other host threads) race and must not
+ * be issued.
+ */
+#define VLC_DECODE_NOALLOC_MAX_BYTES (((int64_t)16) << 20)
+int vlc_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                            int64_t cache_row_stride, int page_size, int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_row_stride, int bt_cols,
+                            const int32_t* cache_seqlens, int batch, int num_heads_q, int num_heads_kv,
+                            int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
+                            void* out, int64_t out_row_stride, void* stream);
 
 #ifdef __cplusplus
 }

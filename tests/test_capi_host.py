@@ -186,3 +186,19 @@ def test_workload_counts_match_hand_derivation():
     assert workloads.merged_grid(1920, 1080) == (39, 69)
     r = workloads.cfg2().requests[0]
     assert (r.R, r.n_reused, r.n_computed, r.delta) == (1055, 9494, 1247, 88)
+
+
+def test_decode_noalloc_refuses_calls_beyond_its_scratch(lib):
+    """600 sequences x 4 kv heads in 2 chunks each need ~40 MB of split partials, more
+    than the fixed 16 MiB scratch: refused before any device call (the fake device
+    addresses below are never touched)."""
+    fake = 1 << 20
+    B, hq, hkv = 600, 28, 4
+    st = lib.vlc_decode_attn_noalloc(fake, hq * 128, fake, fake, hkv * 128, 256, 1000, fake, 64, 64, fake, B, hq,
+                                     hkv, 128, 0.088, 1024, 2, 0x42, fake, hq * 128, None)
+    assert st == _lib.VLC_ERR_SCRATCH
+    assert b"scratch" in lib.vlc_status_string(st)
+    # the same call through the torch wrapper's plan check
+    plan = kernels.plan_decode(B, hq, hkv, 128, 256, 2048, "cpu", num_splits=2, workspace=False)
+    assert plan.grid_splits == 2 and plan.workspace is None
+    assert plan.workspace_bytes > _lib.DECODE_NOALLOC_MAX_BYTES

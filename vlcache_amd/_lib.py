@@ -43,6 +43,10 @@ SIGNATURES = {
         [vp, i64, vp, vp, i64, i32, i64, vp, i64, i32, vp, i32, i32, i32, i32, f32, i32, i32, i32, vp, i64,
          vp, i64, vp],
     ),
+    "vlc_decode_attn_noalloc": (
+        i32,
+        [vp, i64, vp, vp, i64, i32, i64, vp, i64, i32, vp, i32, i32, i32, i32, f32, i32, i32, i32, vp, i64, vp],
+    ),
     "vlc_attn_plan": (
         i32,
         [c_i32p, c_i32p, i32, i32, i32, i32, i32, i32, c_i32p, i64, c_i64p, c_i64p],
@@ -62,6 +66,8 @@ VLC_ERR_UNSUPPORTED = -2
 VLC_ERR_WORKSPACE = -3
 VLC_ERR_CAPACITY = -4
 VLC_ERR_PLAN = -5
+VLC_ERR_SCRATCH = -6
+DECODE_NOALLOC_MAX_BYTES = 16 << 20  # VLC_DECODE_NOALLOC_MAX_BYTES
 
 
 class VLCError(RuntimeError):

@@ -11,6 +11,7 @@ VLC_HOST_API const char* vlc_status_string(int status) {
     case VLC_ERR_WORKSPACE: return "workspace too small for the plan";
     case VLC_ERR_CAPACITY: return "plan buffer too small";
     case VLC_ERR_PLAN: return "plan does not match the call";
+    case VLC_ERR_SCRATCH: return "call needs more than the library's fixed scratch (VLC_DECODE_NOALLOC_MAX_BYTES)";
     default: return status > 0 ? "HIP runtime error" : "unknown status";
   }
 }

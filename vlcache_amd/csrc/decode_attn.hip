@@ -23,6 +23,7 @@
 // partials have landed) merges all chunks with the log-sum-exp rule, writes the
 // output and resets its counter to zero, so one launch does the whole call.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -600,13 +601,64 @@ VLC_API int vlc_decode_attn_plan(int batch, int num_heads_q, int num_heads_kv, i
   return VLC_OK;
 }
 
-VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
-                            int64_t cache_row_stride, int page_size, int64_t num_blocks,
-                            const int32_t* block_table, int64_t bt_row_stride, int bt_cols,
-                            const int32_t* cache_seqlens, int batch, int num_heads_q, int num_heads_kv,
-                            int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
-                            void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
-                            void* stream) {
+namespace {
+// ---- fixed scratch of vlc_decode_attn_noalloc ------------------------------------
+// The ticket counters and split partials of an allocation-free call live in this
+// file-scope device array; every device the library runs on holds its own copy
+// until the process ends.  In host code `scratch` names a host-side stand-in, not
+// a device address: host code uses only the address hipGetSymbolAddress returns
+// for the current device (g_scratch_addr), never the array's name.
+constexpr int64_t kScratchBytes = VLC_DECODE_NOALLOC_MAX_BYTES;
+// The counters sit at the front of the layout ([B * Hkv] words); this much is
+// cleared once per device.  A call whose partials fit the scratch has fewer than
+// kScratchBytes / 16644 < 1024 pairs, so its counters fit in the first 4 KiB.
+constexpr int64_t kScratchClearBytes = int64_t(64) << 10;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxDevices] = {};
+
+__global__ void clear_words_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Address of the current device's scratch.  The first call on a device looks it
+// up (with that device current) and enqueues, on `st`, a kernel that zeroes the
+// counter area (a kernel rather than hipMemsetAsync, so a caller may capture it in
+// a HIP graph; the loader also zero-fills the array, which is uninitialised device
+// data).  Later calls return the cached address.
+int scratch_address(hipStream_t st, void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return VLC_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return VLC_ERR_INVALID;
+    const int64_t words = kScratchClearBytes / 4;
+    hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       static_cast<uint32_t*>(p), words);
+    const int ls = vlc::launch_status();
+    if (ls != VLC_OK) return ls;
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return VLC_OK;
+}
+
+// Shared body of vlc_decode_attn and vlc_decode_attn_noalloc.  use_scratch: the
+// workspace is the device's fixed scratch (workspace/workspace_bytes ignored).
+int decode_attn_run(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                    int64_t cache_row_stride, int page_size, int64_t num_blocks,
+                    const int32_t* block_table, int64_t bt_row_stride, int bt_cols,
+                    const int32_t* cache_seqlens, int batch, int num_heads_q, int num_heads_kv,
+                    int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
+                    void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                    bool use_scratch, void* stream) {
   using namespace vlc;
   if (batch < 0 || num_heads_kv <= 0 || num_heads_q <= 0 || num_heads_q % num_heads_kv != 0)
     return VLC_ERR_INVALID;
@@ -618,7 +670,8 @@ VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_c
   const int waves = sh->waves;
   if (batch == 0) return VLC_OK;
   if (batch > 65535 || num_heads_kv > 65535) return VLC_ERR_UNSUPPORTED;  // grid z / y
-  if (!q || !k_cache || !v_cache || !block_table || !cache_seqlens || !out || !workspace) return VLC_ERR_INVALID;
+  if (!q || !k_cache || !v_cache || !block_table || !cache_seqlens || !out || (!workspace && !use_scratch))
+    return VLC_ERR_INVALID;
   if (key_chunk <= 0 || key_chunk % kWgKeys != 0 || grid_splits <= 0 || grid_splits > 65535 || bt_cols <= 0)
     return VLC_ERR_INVALID;
   if ((int64_t)key_chunk > (int64_t)waves * (kMaxPagesPerWave - 1) * page_size) return VLC_ERR_INVALID;
@@ -627,11 +680,19 @@ VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_c
       cache_row_stride < num_heads_kv * (int64_t)kHeadDim || bt_row_stride < bt_cols || num_blocks <= 0)
     return VLC_ERR_INVALID;
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || q_row_stride % 8 ||
-      out_row_stride % 8 || cache_row_stride % 8 || !aligned16(workspace))
+      out_row_stride % 8 || cache_row_stride % 8 || (!use_scratch && !aligned16(workspace)))
     return VLC_ERR_INVALID;
   int64_t off_ml, off_o, total;
   ws_layout(batch, num_heads_kv, grid_splits, &off_ml, &off_o, &total);
-  if (workspace_bytes < total) return VLC_ERR_WORKSPACE;
+  hipStream_t st = as_stream(stream);
+  if (use_scratch) {
+    // With one chunk per pair the kernel touches no workspace at all.
+    if (grid_splits > 1 && total > kScratchBytes) return VLC_ERR_SCRATCH;
+    const int s = scratch_address(st, &workspace);
+    if (s != VLC_OK) return s;
+  } else if (workspace_bytes < total) {
+    return VLC_ERR_WORKSPACE;
+  }
   decode::Params p;
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k_cache);
@@ -658,7 +719,6 @@ VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_c
   const dim3 grid(grid_splits, num_heads_kv, batch);
   // bytes the call may read: K and V rows of every covered key of every sequence
   const bool nt = (int64_t)batch * p.max_keys * num_heads_kv * kHeadDim * 2 * 2 <= decode::kNtMaxBytes;
-  hipStream_t st = as_stream(stream);
   switch (pipeline) {
 #define VLC_DECODE_CASE(W, S, T)                                                                       \
   case pipeline_code(W, S, T):                                                                         \
@@ -680,4 +740,31 @@ VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_c
     default: return VLC_ERR_INVALID;
   }
   return launch_status();
+}
+}  // namespace
+
+VLC_API int vlc_decode_attn(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                            int64_t cache_row_stride, int page_size, int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_row_stride, int bt_cols,
+                            const int32_t* cache_seqlens, int batch, int num_heads_q, int num_heads_kv,
+                            int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
+                            void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+  return decode_attn_run(q, q_row_stride, k_cache, v_cache, cache_row_stride, page_size, num_blocks, block_table,
+                         bt_row_stride, bt_cols, cache_seqlens, batch, num_heads_q, num_heads_kv, head_dim,
+                         softmax_scale, key_chunk, grid_splits, pipeline, out, out_row_stride, workspace,
+                         workspace_bytes, false, stream);
+}
+
+VLC_API int vlc_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_cache,
+                                    const void* v_cache, int64_t cache_row_stride, int page_size,
+                                    int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
+                                    int bt_cols, const int32_t* cache_seqlens, int batch, int num_heads_q,
+                                    int num_heads_kv, int head_dim, float softmax_scale, int key_chunk,
+                                    int grid_splits, int pipeline, void* out, int64_t out_row_stride,
+                                    void* stream) {
+  return decode_attn_run(q, q_row_stride, k_cache, v_cache, cache_row_stride, page_size, num_blocks, block_table,
+                         bt_row_stride, bt_cols, cache_seqlens, batch, num_heads_q, num_heads_kv, head_dim,
+                         softmax_scale, key_chunk, grid_splits, pipeline, out, out_row_stride, nullptr, 0, true,
+                         stream);
 }

@@ -371,7 +371,8 @@ class DecodePlan:
     key_chunk: int
     grid_splits: int
     pipeline: int
-    workspace: torch.Tensor
+    workspace: torch.Tensor | None
+    workspace_bytes: int = 0
 
 
 def decode_supported(num_heads_q: int, num_heads_kv: int, head_dim: int, page_size: int) -> bool:
@@ -382,12 +383,13 @@ def decode_supported(num_heads_q: int, num_heads_kv: int, head_dim: int, page_si
 
 def plan_decode(batch: int, num_heads_q: int, num_heads_kv: int, head_dim: int, page_size: int,
                 max_seqlen_k: int, device, num_cus: int | None = None, num_splits: int = 0,
-                pipeline: int = 0) -> DecodePlan:
+                pipeline: int = 0, workspace: bool = True) -> DecodePlan:
     """Size a decode launch (vlc_decode_attn_plan) and allocate its zeroed workspace.
 
     pipeline: kernel shape, 16 * waves per workgroup + stages per wave, plus 0x100
     for 16-key tiles (0x42, 0x22, 0x23, 0x24, 0x14, 0x142, 0x144, 0x182, 0x124),
-    0 = the library's choice.
+    0 = the library's choice.  workspace=False sizes the launch only (for
+    decode_attention_noalloc, which allocates nothing); plan.workspace is None.
     """
     lib = _lib.load()
     device = torch.device(device)
@@ -401,23 +403,14 @@ def plan_decode(batch: int, num_heads_q: int, num_heads_kv: int, head_dim: int, 
                                   num_cus, num_splits, pipeline, ctypes.byref(chunk), ctypes.byref(splits),
                                   ctypes.byref(pipe), ctypes.byref(ws))
     _lib.check("vlc_decode_attn_plan", st)
-    workspace = torch.zeros(max(ws.value, 16), dtype=torch.uint8, device=device)
+    buf = torch.zeros(max(ws.value, 16), dtype=torch.uint8, device=device) if workspace else None
     return DecodePlan(batch, num_heads_q, num_heads_kv, page_size, int(max_seqlen_k), chunk.value, splits.value,
-                      pipe.value, workspace)
+                      pipe.value, buf, ws.value)
 
 
-def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_seqlens: torch.Tensor,
-                     block_table: torch.Tensor, softmax_scale: float, plan: DecodePlan | None = None,
-                     max_seqlen_k: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Paged GQA decode attention, one query per sequence (vlc_decode_attn).
-
-    q: [B, Hq, 128] bf16 (any row stride between sequences); k_cache/v_cache:
-    [num_blocks, page, Hkv, 128]; cache_seqlens: int32 [B] on the device;
-    block_table: int32 [B, max_blocks].  The plan must cover the longest length
-    (max_seqlen_k); without one it is built here from max_seqlen_k, or from
-    cache_seqlens (a device-to-host copy).  Returns [B, Hq, 128].
-    """
-    _require_device("decode_attention", q, k_cache, v_cache, cache_seqlens, block_table)
+def _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, out):
+    """Shape checks shared by both decode entry points; returns (B, hq, hkv, page, nblocks)."""
+    _require_device("decode_attention", q, k_cache, v_cache, cache_seqlens, block_table, out)
     B, hq = q.shape[0], q.shape[1]
     hkv = k_cache.shape[-2]
     _check_rows("q", q, hq)
@@ -433,18 +426,44 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
             or block_table.stride(1) != 1:
         raise ValueError("block_table must be int32 [B, max_blocks] with contiguous rows")
-    page, nblocks = k_cache.shape[1], k_cache.shape[0]
+    if out is not None and (out.shape != (B, hq, HEAD_DIM) or out.dtype != torch.bfloat16 or out.stride(-1) != 1
+                            or out.stride(1) != HEAD_DIM):
+        raise ValueError("out must be bf16 [B, Hq, 128] with contiguous head rows")
+    return B, hq, hkv, k_cache.shape[1], k_cache.shape[0]
+
+
+def _check_decode_plan(plan: DecodePlan, B, hq, hkv, page, max_seqlen_k):
+    if (plan.batch, plan.num_heads_q, plan.num_heads_kv, plan.page_size) != (B, hq, hkv, page):
+        raise ValueError("decode plan does not match the call")
+    # The kernel attends at most the keys its grid covers (grid_splits * key_chunk,
+    # i.e. the plan's max_seqlen_k rounded up): a longer context would be cut short.
+    if max_seqlen_k is not None and int(max_seqlen_k) > plan.max_seqlen_k:
+        raise ValueError(f"decode plan covers {plan.max_seqlen_k} keys, the call has contexts up to "
+                         f"{int(max_seqlen_k)}: plan for the longest context")
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_seqlens: torch.Tensor,
+                     block_table: torch.Tensor, softmax_scale: float, plan: DecodePlan | None = None,
+                     max_seqlen_k: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged GQA decode attention, one query per sequence (vlc_decode_attn).
+
+    q: [B, Hq, 128] bf16 (any row stride between sequences); k_cache/v_cache:
+    [num_blocks, page, Hkv, 128]; cache_seqlens: int32 [B] on the device;
+    block_table: int32 [B, max_blocks].  The plan must cover the longest length:
+    max_seqlen_k, when given, is checked against it.  Without a plan one is
+    built here from max_seqlen_k, or from cache_seqlens (a device-to-host copy).
+    Returns [B, Hq, 128].
+    """
+    B, hq, hkv, page, nblocks = _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, out)
     if plan is None:
         if max_seqlen_k is None:
             max_seqlen_k = int(cache_seqlens.max().item()) if B else 0
         plan = plan_decode(B, hq, hkv, HEAD_DIM, page, max_seqlen_k, q.device)
-    if (plan.batch, plan.num_heads_q, plan.num_heads_kv, plan.page_size) != (B, hq, hkv, page):
-        raise ValueError("decode plan does not match the call")
+    _check_decode_plan(plan, B, hq, hkv, page, max_seqlen_k)
+    if plan.workspace is None:
+        raise ValueError("decode plan has no workspace (built with workspace=False): use decode_attention_noalloc")
     if out is None:
         out = torch.empty(B, hq, HEAD_DIM, dtype=torch.bfloat16, device=q.device)
-    elif out.shape != (B, hq, HEAD_DIM) or out.dtype != torch.bfloat16 or out.stride(-1) != 1 \
-            or out.stride(1) != HEAD_DIM:
-        raise ValueError("out must be bf16 [B, Hq, 128] with contiguous head rows")
     ws = plan.workspace
     st = _lib.load().vlc_decode_attn(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(1), page, nblocks,
@@ -452,4 +471,31 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         HEAD_DIM, float(softmax_scale), plan.key_chunk, plan.grid_splits, plan.pipeline, out.data_ptr(), out.stride(0),
         ws.data_ptr(), ws.numel(), _stream(q))
     _lib.check("vlc_decode_attn", st)
+    return out
+
+
+def decode_attention_noalloc(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             cache_seqlens: torch.Tensor, block_table: torch.Tensor, softmax_scale: float,
+                             plan: DecodePlan, out: torch.Tensor, max_seqlen_k: int | None = None) -> torch.Tensor:
+    """decode_attention through vlc_decode_attn_noalloc: nothing is allocated.
+
+    For callers that cannot allocate device memory (HIP graph capture, tight
+    serving loops).  The split partials and ticket counters live in the
+    library's fixed per-device scratch (DECODE_NOALLOC_MAX_BYTES); out is
+    required; the plan only sizes the launch (plan_decode(..., workspace=False)
+    builds one without a buffer).  Calls that overlap on one device race.
+    """
+    if out is None:
+        raise ValueError("decode_attention_noalloc writes into a caller-supplied out")
+    B, hq, hkv, page, nblocks = _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, out)
+    _check_decode_plan(plan, B, hq, hkv, page, max_seqlen_k)
+    if plan.grid_splits > 1 and plan.workspace_bytes > _lib.DECODE_NOALLOC_MAX_BYTES:
+        raise ValueError(f"decode call needs {plan.workspace_bytes} bytes of scratch, more than the "
+                         f"{_lib.DECODE_NOALLOC_MAX_BYTES} of the allocation-free entry point")
+    st = _lib.load().vlc_decode_attn_noalloc(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(1), page, nblocks,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], cache_seqlens.data_ptr(), B, hq, hkv,
+        HEAD_DIM, float(softmax_scale), plan.key_chunk, plan.grid_splits, plan.pipeline, out.data_ptr(), out.stride(0),
+        _stream(q))
+    _lib.check("vlc_decode_attn_noalloc", st)
     return out

@@ -94,7 +94,8 @@ class Attention(nn.Module):
         # decode: one query per sequence against its cached context (layers/attention.py:71-74)
         if kernels.decode_supported(self.num_heads, self.num_kv_heads, self.head_dim, k_cache.shape[1]):
             plan = context.decode_plan
-            if plan is None or plan.batch != q.shape[0] or plan.num_heads_q != self.num_heads:
+            if plan is None or plan.batch != q.shape[0] or plan.num_heads_q != self.num_heads or \
+                    (context.max_seqlen_k or 0) > plan.max_seqlen_k:
                 max_k = context.max_seqlen_k or None
                 if context.cu_seqlens_k_host is not None:
                     cu = context.cu_seqlens_k_host
@@ -104,7 +105,7 @@ class Attention(nn.Module):
                                            int(context.context_lens.max().item()), q.device)
                 context.decode_plan = plan
             o = kernels.decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables,
-                                         self.scale, plan=plan)
+                                         self.scale, plan=plan, max_seqlen_k=context.max_seqlen_k or None)
         else:  # shapes the decode kernel does not take: the varlen kernel with one query per sequence
             plan = _plan(context, self.num_heads, self.num_kv_heads, self.head_dim, q.device)
             o = kernels.varlen_attention(q, k_cache, v_cache, context.cu_seqlens_q, context.cu_seqlens_k,
