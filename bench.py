@@ -283,7 +283,8 @@ def run_ttft(ratio: float, reps: int = 2):
     from vlcache_amd.config import QWEN25_VL_3B
 
     img_tok = QWEN25_VL_3B["image_token_id"]
-    llm = LLM(dict(QWEN25_VL_3B), recompute_ratio=ratio, num_kvcache_blocks=8 * 43, enforce_eager=True)
+    llm = LLM(dict(QWEN25_VL_3B), recompute_ratio=ratio, num_kvcache_blocks=8 * 43, enforce_eager=True,
+              synthetic_vision=True)
     sp = SamplingParams(temperature=0.6, max_tokens=1)
     grid = torch.tensor([[1, 154, 274]])
     n_img = 77 * 137

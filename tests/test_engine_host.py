@@ -55,10 +55,10 @@ def test_block_manager_partial_decision_and_refcounts():
     assert not bm.try_partial_recompute(a)            # registry miss
     bm.allocate(a)
     a.find_image_token_range(IMG)
-    a.image_rope_start = (40, 40, 40)
+    a.set_rope_starts([(40, 40, 40)])
     bm.store_image_kv(a)
     img_blocks = a.block_table[40 // 256:(40 + 1024 - 1) // 256 + 1]
-    assert all(bm.blocks[b].ref_count == 2 for b in img_blocks)
+    assert all(bm.ref_count(b) == 2 for b in img_blocks)
     b = _seq(128, 1024, 64)
     assert bm.try_partial_recompute(b)
     assert b.num_recompute_tokens == op.recompute_count(0.1, 1024) == 103
@@ -68,10 +68,11 @@ def test_block_manager_partial_decision_and_refcounts():
     assert not bm.try_partial_recompute(c)
     # the image blocks outlive the source sequence
     bm.deallocate(a)
-    assert all(bm.blocks[x].ref_count == 1 for x in img_blocks)
-    free_before = len(bm.free_block_ids)
-    bm._release_image_blocks(entry)
-    assert len(bm.free_block_ids) == free_before + len(img_blocks)
+    assert all(bm.ref_count(x) == 1 for x in img_blocks)
+    free_before = bm.num_free_blocks
+    assert bm.release_image(7) and not bm.release_image(7)
+    assert bm.num_free_blocks == free_before + len(img_blocks)
+    assert bm.free_block_ids()[-len(img_blocks):] == img_blocks
 
 
 def test_config_from_dict_and_directory(tmp_path):
@@ -144,7 +145,7 @@ def test_block_manager_per_image_decision_registry_and_budget():
     assert not bm.try_partial_recompute(a)            # registry miss for both
     bm.allocate(a)
     a.find_image_token_range(IMG)
-    a.image_rope_starts = [(40, 40, 40), (90, 90, 90)]
+    a.set_rope_starts([(40, 40, 40), (90, 90, 90)])
     bm.store_image_kv(a)
     e7, e8 = bm.get_image_kv_entry(7), bm.get_image_kv_entry(8)
     assert (e7.img_start, e7.img_end, e7.rope_start) == (40, 1064, (40, 40, 40))
@@ -180,12 +181,12 @@ def test_image_kv_copy_plan_matches_oracle_slots():
     src, _ = _multi([("text", 64), ("image", 2691), ("text", 64), ("image", 700), ("text", 9)], [11, 12])
     bm.allocate(src)
     src.find_image_token_range(IMG)
-    src.image_rope_starts = [(64, 64, 64), (200, 200, 200)]
+    src.set_rope_starts([(64, 64, 64), (200, 200, 200)])
     bm.store_image_kv(src)
     dst, ranges = _multi([("text", 100), ("image", 700), ("text", 30), ("image", 2691), ("text", 64)], [12, 11])
     assert bm.try_partial_recompute(dst)
     bm.allocate(dst)
-    dst.image_rope_starts = [(100, 100, 100), (180, 180, 180)]
+    dst.set_rope_starts([(100, 100, 100), (180, 180, 180)])
     old, new, deltas, seg = image_kv_copy_plan([dst], bm)
     exp_old, exp_new, exp_seg = [], [], []
     for k, ((s, e), h) in enumerate(zip(ranges, [12, 11])):
@@ -197,3 +198,182 @@ def test_image_kv_copy_plan_matches_oracle_slots():
         exp_seg += [k] * len(o)
     assert old.tolist() == exp_old and new.tolist() == exp_new and seg.tolist() == exp_seg
     assert deltas == [[100 - 200] * 3, [180 - 64] * 3]
+
+
+# ----------------------------------------------------------------------------- pool and scheduler vs the oracle
+def _run_oracle(reqs, num_blocks, max_seqs, budget):
+    from oracle import engine as oe
+
+    sch = oe.Scheduler(num_blocks, 256, max_seqs, budget)
+    seqs = [oe.Seq(i, p, m) for i, (p, m) in enumerate(reqs)]
+    sch.waiting.extend(seqs)
+    steps = []
+    while sch.waiting or sch.running:
+        batch, prefill = sch.schedule()
+        steps.append(([s.seq_id for s in batch], prefill, [list(s.block_table) for s in batch]))
+        sch.postprocess(batch)
+        assert len(steps) < 10000
+    return steps
+
+
+def _run_product(reqs, num_blocks, max_seqs, budget):
+    from vlcache_amd import SamplingParams
+    from vlcache_amd.engine.scheduler import Scheduler
+
+    cfg = Config(dict(QWEN25_VL_3B), num_kvcache_blocks=num_blocks, max_num_seqs=max_seqs,
+                 max_num_batched_tokens=budget, max_model_len=budget)
+    sch = Scheduler(cfg)
+    seqs = [Sequence([5] * p, SamplingParams(max_tokens=m, ignore_eos=True)) for p, m in reqs]
+    index = {s.seq_id: i for i, s in enumerate(seqs)}
+    for s in seqs:
+        sch.add(s)
+    steps = []
+    while not sch.is_finished():
+        batch, prefill = sch.schedule()
+        steps.append(([index[s.seq_id] for s in batch], prefill, [list(s.block_table) for s in batch]))
+        sch.postprocess(batch, [7] * len(batch))
+        assert len(steps) < 10000
+    assert sch.block_manager.num_free_blocks == num_blocks and not sch.block_manager.ref_counts.any()
+    return steps
+
+
+def test_oracle_scheduler_known_answer():
+    # 3 blocks; A and B: 256-token prompts, 3 new tokens each.  Hand-derived:
+    # prefill [A, B] (1 block each); decode: A opens a block, B finds none and, being the
+    # last left, preempts itself; decode [A]; A finishes; B is prefilled again (257
+    # tokens, 2 blocks); decode [B] finishes it.
+    steps = _run_oracle([(256, 3), (256, 3)], 3, 8, 4096)
+    assert [(ids, pf) for ids, pf, _ in steps] == [([0, 1], True), ([0], False), ([0], False), ([1], True),
+                                                  ([1], False)]
+    assert steps[0][2] == [[0], [1]] and steps[1][2] == [[0, 2]]
+    # freed blocks come back in release order: B's 1, then A's table last to first (2, 0)
+    assert steps[3][2] == [[1, 2]]
+
+
+def test_scheduler_matches_oracle_known_answer():
+    assert _run_product([(256, 3), (256, 3)], 3, 8, 4096) == _run_oracle([(256, 3), (256, 3)], 3, 8, 4096)
+
+
+@pytest.mark.parametrize("seed", range(25))
+def test_scheduler_matches_oracle_random(seed):
+    """Random request mixes under tight pools (preemption), small batch caps and budgets:
+    every step's batch, kind and block tables equal the reference's loop."""
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 9))
+    reqs = [(int(rng.integers(1, 900)), int(rng.integers(1, 300))) for _ in range(n)]
+    need = max(-(-(p + m) // 256) for p, m in reqs)
+    num_blocks = int(rng.integers(need, need + 8))
+    max_seqs = int(rng.integers(1, 6))
+    budget = int(rng.integers(max(p for p, _ in reqs) + 300, 4096))
+    o = _run_oracle(reqs, num_blocks, max_seqs, budget)
+    p = _run_product(reqs, num_blocks, max_seqs, budget)
+    assert p == o
+
+
+def test_pool_ring_wraps_and_refuses_overdraw():
+    bm = BlockManager(num_blocks=4, block_size=256)
+    s1, s2 = Sequence([1] * 700), Sequence([1] * 200)
+    bm.allocate(s1)
+    bm.allocate(s2)
+    assert s1.block_table == [0, 1, 2] and s2.block_table == [3] and bm.num_free_blocks == 0
+    bm.deallocate(s1)
+    assert bm.free_block_ids() == [2, 1, 0]
+    s3 = Sequence([1] * 300)
+    bm.allocate(s3)
+    assert s3.block_table == [2, 1] and bm.free_block_ids() == [0]
+    with pytest.raises(RuntimeError):
+        bm.allocate(Sequence([1] * 600))
+    bm.deallocate(s2)
+    bm.deallocate(s3)
+    assert bm.free_block_ids() == [0, 3, 1, 2] and not bm.ref_counts.any()
+
+
+# ----------------------------------------------------------------------------- positions after preemption
+def test_positions_continue_past_the_prompt_after_preemption():
+    """A prompt with an image, 5 generated tokens, then a preemption: the prefill of all
+    len(seq) tokens gets one position column per token; past the prompt index p sits at
+    p + rope_delta on every row (the decode rule), so the columns continue the prompt's."""
+    toks = [1] * 5 + [IMG] * 15 + [2] * 3
+    seq = Sequence(toks)
+    pos, starts, delta = mrope_positions(toks, [(1, 6, 10)], IMG)
+    seq.rope_positions, seq.rope_delta = pos, delta
+    for t in range(5):
+        seq.append_token(100 + t)
+    got = seq.positions(0, len(seq), True)
+    assert got.shape == (3, len(seq))
+    assert np.array_equal(got[:, :len(toks)], pos)
+    tail = np.arange(len(toks), len(seq)) + delta
+    assert np.array_equal(got[:, len(toks):], np.tile(tail, (3, 1)))
+    assert tail[0] == pos.max() + 1  # the first generated token follows the prompt's last position
+    assert np.array_equal(seq.positions(20, 26, False), np.concatenate([pos[0, 20:23], tail[:3]]))
+    # through the scheduler: prefill, 5 decode tokens, preemption, prefill again
+    from vlcache_amd import SamplingParams
+    from vlcache_amd.engine.scheduler import Scheduler
+
+    cfg = Config(dict(QWEN25_VL_3B, image_token_id=IMG), num_kvcache_blocks=4, max_model_len=4096)
+    sch = Scheduler(cfg)
+    s = Sequence(toks, SamplingParams(max_tokens=50, ignore_eos=True))
+    s.rope_positions, s.rope_delta = pos, delta
+    sch.add(s)
+    sch.schedule()
+    sch.postprocess([s], [9])
+    for _ in range(4):
+        batch, prefill = sch.schedule()
+        assert not prefill
+        sch.postprocess(batch, [9])
+    sch.preempt(s)
+    batch, prefill = sch.schedule()
+    assert prefill and batch == [s] and s.computed_runs() == [(0, len(s))]
+    assert s.positions(0, len(s), True).shape == (3, len(toks) + 5)
+
+
+# ----------------------------------------------------------------------------- encoder cache
+def test_encoder_cache_lru_views_and_limits():
+    import torch
+
+    from vlcache_amd.engine.encoder_cache import EncoderCache
+
+    ec = EncoderCache(num_pages=6, page_rows=4, hidden=3, dtype=torch.float32, device="cpu")
+    a = torch.arange(10 * 3, dtype=torch.float32).view(10, 3)  # 3 pages
+    b = -torch.arange(5 * 3, dtype=torch.float32).view(5, 3)   # 2 pages
+    assert ec.put(1, a) and ec.put(2, b) and ec.free_pages == 1
+    got = ec.get(1, 6)
+    assert torch.equal(got, a[:6]) and got.data_ptr() == ec.pool.data_ptr()  # a view, no gather
+    assert torch.equal(ec.get(2), b)
+    c = torch.ones(7, 3)                                       # 2 pages: evicts the least recent (1)
+    assert ec.put(3, c) and 1 not in ec and 2 in ec and ec.evictions == 1
+    assert ec.get(1) is None and ec.misses == 1
+    d = torch.full((4, 3), 5.0)                                # 1 page, fits without eviction
+    assert ec.put(4, d)
+    # entry 3 took pages 0, 1 (freed by 1) and entry 4 page 2: a read of 3 is a view again
+    assert torch.equal(ec.get(3), c)
+    ec2 = EncoderCache(num_pages=4, page_rows=2, hidden=1, dtype=torch.float32, device="cpu")
+    ec2.put(1, torch.zeros(2, 1))
+    ec2.put(2, torch.ones(2, 1))
+    ec2.put(3, torch.full((2, 1), 2.0))
+    ec2.get(1)
+    ec2.put(4, torch.full((4, 1), 3.0))   # needs 2 pages, 1 free: evicts 2, the least recent
+    assert sorted(k for k in (1, 2, 3, 4) if k in ec2) == [1, 3, 4] and ec2.evictions == 1
+    ec2._free[:] = True
+    ec2._entries.clear()
+    ec2._last_use.clear()
+    ec2.put(5, torch.zeros(2, 1))         # page 0
+    ec2.put(6, torch.zeros(2, 1))         # page 1
+    ec2.put(7, torch.zeros(2, 1))         # page 2
+    ec2._free[1] = True                   # a hole: 8 lands on pages 1 and 3 (a gather to read)
+    del ec2._entries[6], ec2._last_use[6]
+    e = torch.tensor([[1.0], [2.0], [3.0], [4.0]])
+    assert ec2.put(8, e) and torch.equal(ec2.get(8), e) and torch.equal(ec2.get(8, 3), e[:3])
+    assert not ec2.put(9, torch.zeros(9, 1))  # larger than the pool: not cached
+
+
+def test_runner_refuses_token_ids_outside_the_vocabulary():
+    from types import SimpleNamespace
+
+    from vlcache_amd.engine.model_runner import ModelRunner
+
+    stub = SimpleNamespace(config=SimpleNamespace(hf_config=SimpleNamespace(vocab_size=1000)))
+    assert ModelRunner._checked_ids(stub, np.array([0, 5, 999])).tolist() == [0, 5, 999]
+    for bad in ([1, 151655], [-1, 3]):
+        with pytest.raises(ValueError, match="outside the vocabulary"):
+            ModelRunner._checked_ids(stub, np.array(bad))

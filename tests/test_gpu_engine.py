@@ -96,6 +96,7 @@ def _engine(ratio, blocks=64, seed=0):
     from vlcache_amd import LLM
 
     return LLM(dict(TINY), recompute_ratio=ratio, num_kvcache_blocks=blocks, max_model_len=4096, seed=seed,
+               synthetic_vision=True,
                enforce_eager=True)
 
 

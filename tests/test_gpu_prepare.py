@@ -26,8 +26,10 @@ from vlcache_amd.utils.context import get_context, reset_context
 pytestmark = pytest.mark.gpu
 
 IMG = 151655
+# vocab_size covers the image token id: the model embeds every prompt id before the image
+# rows are replaced by visual embeddings.
 SMALL = dict(hidden_size=256, intermediate_size=512, num_hidden_layers=1, num_attention_heads=2,
-             num_key_value_heads=1, vocab_size=1000, rms_norm_eps=1e-6, rope_theta=1e6,
+             num_key_value_heads=1, vocab_size=151936, rms_norm_eps=1e-6, rope_theta=1e6,
              rope_scaling={"type": "mrope", "mrope_section": [16, 24, 24]}, max_position_embeddings=32768,
              tie_word_embeddings=True, image_token_id=IMG, spatial_merge_size=2, eos_token_id=0,
              torch_dtype="bfloat16", head_dim=128)
@@ -133,3 +135,68 @@ def test_prepare_prefill_mixed_batch(dev):
     exp = _check(eng, seqs)
     assert exp.logit_indices == [1, 2, 4]
     assert len(exp.block_tables) == 5  # the text-only prompt reads the paged cache too
+
+
+def test_prepare_prefill_after_preemption_mrope(dev):
+    """An image prompt in M-RoPE mode, five decoded tokens, a preemption, then the prefill
+    of all its tokens again: one position column per token, the prompt's rows followed by
+    index + rope_delta on every row."""
+    from vlcache_amd import LLM
+    from vlcache_amd.engine.positions import mrope_positions
+
+    say("prepare_prefill: M-RoPE prompt with an image, preempted after 5 decode steps, prefilled again")
+    eng = LLM(dict(SMALL), recompute_ratio=0.0, num_kvcache_blocks=8, max_model_len=4096, enforce_eager=True)
+    toks, mm = _prompt(20, (1, 12, 16), 9, seed=8)
+    seq = eng.add_request(toks, SamplingParams(max_tokens=50, ignore_eos=True), mm)
+    sch = eng.scheduler
+    sch.schedule()
+    sch.postprocess([seq], [11])
+    for _ in range(4):
+        batch, prefill = sch.schedule()
+        assert not prefill
+        sch.postprocess(batch, [11])
+    sch.preempt(seq)
+    seqs, prefill = sch.schedule()
+    assert prefill and seqs == [seq] and len(seq) == len(toks) + 5
+    _, pos, _ = eng.model_runner.prepare_prefill(seqs)
+    reset_context()
+    pos = pos.cpu().numpy()
+    ref, _, delta = mrope_positions(toks, [(1, 12, 16)], IMG, 2)
+    assert pos.shape == (3, len(seq))
+    assert (pos[:, :len(toks)] == ref).all()
+    assert (pos[:, len(toks):] == np.arange(len(toks), len(seq)) + delta).all()
+
+
+def test_encoder_cache_miss_without_embeddings_raises(dev):
+    """The vision tower is not part of this path: a cold image with no image_embeds and no
+    synthetic opt-in is an error, not silently made-up embeddings."""
+    say("engine: encoder-cache miss without image_embeds raises")
+    from vlcache_amd import LLM
+
+    eng = LLM(dict(SMALL), recompute_ratio=0.1, num_kvcache_blocks=8, max_model_len=4096, enforce_eager=True)
+    toks, mm = _prompt(10, (1, 8, 8), 4, seed=9)
+    eng.add_request(toks, SamplingParams(max_tokens=1), mm)
+    with pytest.raises(RuntimeError, match="encoder cache"):
+        eng.step()
+    reset_context()
+    # with the caller's embeddings the same request runs and fills the cache
+    eng2 = LLM(dict(SMALL), recompute_ratio=0.1, num_kvcache_blocks=8, max_model_len=4096, enforce_eager=True)
+    emb = torch.randn(16, SMALL["hidden_size"]).to(torch.bfloat16)
+    mm2 = dict(mm, image_embeds=[emb])
+    out = eng2.generate([toks], SamplingParams(max_tokens=1), [mm2])
+    assert len(out) == 1 and len(eng2.model_runner.encoder_cache) == 1
+    cached = eng2.model_runner.encoder_cache.get(next(iter(eng2.model_runner.encoder_cache._entries)))
+    assert torch.equal(cached.cpu(), emb)
+
+
+def test_token_ids_outside_the_vocabulary_are_refused(dev):
+    """An id the embedding table does not have is a host-side error, raised before any
+    device work."""
+    say("engine: token id outside the vocabulary is refused on the host")
+    from vlcache_amd import LLM
+
+    eng = LLM(dict(SMALL, vocab_size=1000), num_kvcache_blocks=4, max_model_len=4096, enforce_eager=True)
+    eng.add_request([1, 2, 5000, 3], SamplingParams(max_tokens=1))
+    with pytest.raises(ValueError, match="outside the vocabulary"):
+        eng.step()
+    reset_context()

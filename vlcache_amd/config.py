@@ -72,6 +72,7 @@ class Config:
     use_mrope: bool = True      # M-RoPE positions when the model config has mrope_section
     rerotate_reused_kv: bool = True  # re-rotate reused image K to its new position
     seed: int = 0               # weights of a model directory without checkpoint files
+    synthetic_vision: bool = False  # encoder-cache miss without image_embeds: seeded synthetic embeddings
     extra: dict = field(default_factory=dict)
 
     def __post_init__(self):

@@ -12,6 +12,12 @@ prepare_sample, run_model, run, allocate_kv_cache, exit.  Differences:
   * positions are M-RoPE [3, N] when the model config has mrope_section and
     use_mrope is set, else the reference's 1-D positions;
   * host preparation is vectorised (numpy) instead of per-token Python loops;
+  * visual embeddings come from a bounded encoder cache (engine/encoder_cache.py)
+    sized by encoder_cache_ratio; the vision tower is not part of this path, so a
+    miss takes the caller's image_embeds, or seeded synthetic embeddings only when
+    the config opts in (synthetic_vision), and raises otherwise;
+  * every decode plan shares one workspace sized once for max_num_seqs requests
+    of up to max_model_len tokens;
   * no tensor parallelism, no shared-memory RPC: one process, one GPU.
 """
 from __future__ import annotations
@@ -21,6 +27,7 @@ import torch
 
 from .. import kernels
 from ..config import Config
+from .encoder_cache import EncoderCache
 from ..qwen_vl import Qwen2_5_VLForConditionalGeneration, Sampler, random_init_
 from ..utils.context import get_context, reset_context, set_context
 from .sequence import Sequence
@@ -64,13 +71,13 @@ class ModelRunner:
         random_init_(self.model, seed=config.seed)
         self.model.eval()
         self.sampler = Sampler()
-        self.encoder_cache: dict[int, torch.Tensor] = {}
         self.num_layers = hf.num_hidden_layers
         self.num_kv_heads = hf.num_key_value_heads
         self.num_heads = hf.num_attention_heads
         self.head_dim = hf.head_dim
         self._logit_indices = None
         self._decode_plans: dict = {}
+        self._decode_workspace = None
         self.allocate_kv_cache()
 
     def call(self, method_name, *args):
@@ -81,14 +88,25 @@ class ModelRunner:
 
     # ------------------------------------------------------------------ memory
     def allocate_kv_cache(self):
+        """KV cache and encoder cache.  Without an explicit block count the memory left
+        under gpu_memory_utilization is split: encoder_cache_ratio of it to the encoder
+        cache, the rest to KV blocks (engine/model_runner.py:126-149); with an explicit
+        count the encoder cache gets the same ratio relative to the KV cache's share."""
         config = self.config
+        hf = config.hf_config
         block_bytes = 2 * self.num_layers * self.block_size * self.num_kv_heads * self.head_dim * self.dtype.itemsize
+        ratio = min(max(config.encoder_cache_ratio, 0.0), 0.95)
         if config.num_kvcache_blocks <= 0:
             free, total = torch.cuda.mem_get_info()
             budget = free - total * (1.0 - config.gpu_memory_utilization)
-            budget *= 1.0 - config.encoder_cache_ratio
-            config.num_kvcache_blocks = int(budget) // block_bytes
+            encoder_bytes = budget * ratio
+            config.num_kvcache_blocks = int(budget - encoder_bytes) // block_bytes
+        else:
+            encoder_bytes = config.num_kvcache_blocks * block_bytes * ratio / (1.0 - ratio)
         assert config.num_kvcache_blocks > 0
+        page_bytes = self.block_size * hf.hidden_size * self.dtype.itemsize
+        self.encoder_cache = EncoderCache(max(0, int(encoder_bytes) // page_bytes), self.block_size,
+                                          hf.hidden_size, self.dtype, self.device)
         self.kv_cache = torch.empty(2, self.num_layers, config.num_kvcache_blocks, self.block_size,
                                     self.num_kv_heads, self.head_dim, dtype=self.dtype, device=self.device)
         layer_id = 0
@@ -123,12 +141,17 @@ class ModelRunner:
         kernels.rerotate_copy_kv(self.kv_cache, old_t, new_t, cos_sin, seg, rotate_k=rotate)
 
     # ------------------------------------------------------------------ step preparation
+    def _checked_ids(self, ids: np.ndarray) -> np.ndarray:
+        """Token ids must index the embedding table: an id outside [0, vocab_size) is refused
+        here rather than read out of bounds on the device."""
+        vocab = self.config.hf_config.vocab_size
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= vocab):
+            bad = int(ids[(ids < 0) | (ids >= vocab)][0])
+            raise ValueError(f"token id {bad} is outside the vocabulary [0, {vocab})")
+        return ids
+
     def _positions(self, seq: Sequence, start: int, end: int) -> np.ndarray:
-        pos = getattr(seq, "rope_positions", None)
-        if pos is None:
-            p = np.arange(start, end, dtype=np.int64)
-            return np.tile(p, (3, 1)) if self.config.use_mrope else p
-        return pos[:, start:end] if self.config.use_mrope else pos[0, start:end]
+        return seq.positions(start, end, self.config.use_mrope)
 
     def prepare_prefill(self, seqs: list[Sequence]):
         input_ids, positions, slot_mapping = [], [], []
@@ -151,7 +174,7 @@ class ModelRunner:
                     mm["image_hashes"].append(seq.image_hashes[i])
                     mm["image_grid_thw"].append(tuple(int(x) for x in grids[i]))
                     mm["image_embeds"].append(None if embeds is None else embeds[i])
-                    r = seq.image_recompute[i] if seq.is_partial_recompute and i < len(seq.image_recompute) else None
+                    r = seq.images[i].recompute if i < len(seq.images) else None
                     mm["recompute"].append(r if r is not None else 0)
             if seq.is_partial_recompute:
                 has_partial = True
@@ -186,7 +209,7 @@ class ModelRunner:
             for i, row in enumerate(vbts):
                 bt[i, :len(row)] = row
             block_tables = _h2d(bt, torch.int32, self.device)
-        input_ids = _h2d(np.concatenate(input_ids), torch.int64, self.device)
+        input_ids = _h2d(self._checked_ids(np.concatenate(input_ids)), torch.int64, self.device)
         positions = _h2d(np.concatenate(positions, axis=-1), torch.int64, self.device)
         cu_q_t = _h2d(np.asarray(cu_q), torch.int32, self.device)
         cu_k_t = _h2d(np.asarray(cu_k), torch.int32, self.device)
@@ -200,7 +223,7 @@ class ModelRunner:
 
     def prepare_decode(self, seqs: list[Sequence]):
         n = len(seqs)
-        input_ids = np.array([s.last_token for s in seqs], dtype=np.int64)
+        input_ids = self._checked_ids(np.array([s.last_token for s in seqs], dtype=np.int64))
         lens = np.array([len(s) for s in seqs], dtype=np.int64)
         pos = lens - 1
         if self.config.use_mrope:
@@ -228,48 +251,75 @@ class ModelRunner:
 
     def _decode_plan(self, batch: int, max_len: int):
         """Decode launch plan for this batch size, sized for contexts up to the next multiple of
-        1024 tokens and reused across steps (its workspace counters return to zero after
-        every call)."""
+        1024 tokens.  Plans are host records; all of them share one workspace, allocated
+        zeroed once for the largest any batch of at most max_num_seqs requests and
+        max_model_len tokens needs (every call leaves its ticket counters at zero)."""
         cap = -(-max(max_len, 1) // 1024) * 1024
         key = (batch, cap)
         plan = self._decode_plans.get(key)
         if plan is None:
             plan = kernels.plan_decode(batch, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size,
-                                       cap, self.device)
+                                       cap, self.device, workspace=False)
+            if self._decode_workspace is None:
+                self._decode_workspace = torch.zeros(self._decode_workspace_bytes(), dtype=torch.uint8,
+                                                     device=self.device)
+            if plan.workspace_bytes > self._decode_workspace.numel():  # contexts beyond max_model_len
+                self._decode_workspace = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device=self.device)
+                self._decode_plans.clear()
+            plan.workspace = self._decode_workspace
+            if len(self._decode_plans) > 4096:
+                self._decode_plans.clear()
             self._decode_plans[key] = plan
         return plan
+
+    def _decode_workspace_bytes(self) -> int:
+        cap = -(-max(self.config.max_model_len, 1) // 1024) * 1024
+        need = 16
+        for b in range(1, max(1, self.config.max_num_seqs) + 1):
+            p = kernels.plan_decode(b, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size, cap,
+                                    self.device, workspace=False)
+            need = max(need, p.workspace_bytes)
+        return need
 
     def prepare_sample(self, seqs: list[Sequence]):
         return _h2d(np.array([s.temperature for s in seqs], dtype=np.float32), torch.float32, self.device)
 
     # ------------------------------------------------------------------ vision inputs
-    def _image_embeds(self, h: int, grid, given):
-        """Visual embeddings of one image: encoder-cache hit, caller-supplied, or synthetic.
+    def _image_embeds(self, h: int, grid, given, rows: int | None):
+        """The first `rows` (all when None) visual embeddings of one image.
 
-        The vision tower is not part of this path.  On a miss the caller's
-        `image_embeds` are used, else seeded synthetic embeddings stand in for its
-        output; either way they are written to the encoder cache.
+        An encoder-cache hit reads them back (engine/model_runner.py:366-372); on a
+        miss the caller's `image_embeds` are used, or seeded synthetic embeddings
+        when Config.synthetic_vision opts in, and are stored in the cache.  The
+        vision tower is not part of this path: a miss with neither raises.
         """
-        if h in self.encoder_cache:
-            return self.encoder_cache[h], 0.0
+        hit = self.encoder_cache.get(h, rows)
+        if hit is not None:
+            return hit
         m = self.config.hf_config.spatial_merge_size
         n = int(grid[0]) * (int(grid[1]) // m) * (int(grid[2]) // m)
         if given is not None:
             emb = given.to(self.device, self.dtype)
-        else:
+        elif self.config.synthetic_vision:
             g = torch.Generator(device=self.device)
             g.manual_seed(h & ((1 << 63) - 1))
             emb = torch.randn(n, self.config.hf_config.hidden_size, generator=g, device=self.device,
                               dtype=self.dtype)
-        assert emb.shape[0] == n
-        self.encoder_cache[h] = emb
-        return emb, 0.0
+        else:
+            raise RuntimeError(
+                f"image {h:#x} is not in the encoder cache and the request carries no image_embeds: the "
+                "vision tower is not part of this build (pass mm_inputs['image_embeds'], or construct the "
+                "engine with synthetic_vision=True for synthetic embeddings)")
+        if emb.shape[0] != n:
+            raise ValueError(f"image_embeds has {emb.shape[0]} rows, the grid {tuple(grid)} gives {n}")
+        self.encoder_cache.put(h, emb)
+        return emb if rows is None else emb[:rows]
 
     def _process_visual(self, mm: dict):
         parts = []
         for h, grid, given, r in zip(mm["image_hashes"], mm["image_grid_thw"], mm["image_embeds"], mm["recompute"]):
-            emb, _ = self._image_embeds(h, grid, given)
-            parts.append(emb[:r] if r > 0 else emb)  # partial: first R embeddings (model_runner.py:398-403)
+            # a reused image needs only its first R embeddings (engine/model_runner.py:398-403)
+            parts.append(self._image_embeds(h, grid, given, r if r > 0 else None))
         return torch.cat(parts, dim=0) if parts else None
 
     # ------------------------------------------------------------------ execution
