@@ -268,6 +268,81 @@ def run_gpu(steps: int, warmup: int, wl_name: str = "cfg2"):
     )
 
 
+def _cold_ms(fn, flush, reps=5, dirty=False):
+    """Median GPU time of fn() after a 512 MiB read (MALL left holding clean lines) or
+    write (dirty lines), with the events behind a GPU spin."""
+    ts = []
+    for _ in range(reps):
+        if dirty:
+            flush.fill_(1)
+        else:
+            flush.view(torch.int64).sum()
+        _gpu_busy()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def run_config(wl_name: str, steps: int, warmup: int, scatter: bool = False):
+    """The other workloads' kernels, each timed as in the main line: attention and the
+    fused RoPE + store as the step's per-layer calls in one HIP graph (per call), the
+    re-rotation cold (median of 5)."""
+    from vlcache_amd import workloads
+    from vlcache_amd.hotpath import WarmPrefillHotPath
+
+    wl = getattr(workloads, wl_name)()
+    hp = WarmPrefillHotPath(wl, "cuda:0", seed=0)
+    m = wl.model
+    L = m.num_layers
+    for _ in range(warmup):
+        hp.step()
+    torch.cuda.synchronize()
+    reps = max(2, min(steps, 5))
+    at_us = _graph_us_per_call(hp.attention, L, reps)
+    rs_us = _graph_us_per_call(hp.rope_store, L, reps)
+    flops = workloads.attention_flops(hp.cu_q_host, hp.cu_k_host, m.num_heads, m.head_dim)
+    tflops = flops / (at_us * 1e-6) / 1e12
+    rs_bytes = workloads.rope_store_bytes(hp.n_computed, m.num_heads, m.num_kv_heads, m.head_dim)
+    out = {
+        "workload": f"{wl.name}: {m.name}, {L} layers, heads {m.num_heads}/{m.num_kv_heads}, "
+                    f"{len(wl.requests)} request(s), {hp.n_computed} computed / {hp.n_reused} reused tokens, "
+                    f"{len(hp.cu_q_host) - 1} virtual sub-sequences",
+        "attention": {"us_per_layer": round(at_us, 2), "gflop_per_layer": round(flops / 1e9, 3),
+                      "tflops": round(tflops, 1), "frac_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                      "work_items": hp.plan.num_items, "split_combines": hp.plan.num_combine,
+                      "paged": hp.paged},
+        "rope_store": {"us_per_layer": round(rs_us, 2), "bytes": rs_bytes,
+                       "gbps": round(rs_bytes / (rs_us * 1e-6) / 1e9, 1),
+                       "frac_hbm_peak": round(rs_bytes / (rs_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "timing": "per call: the step's per-layer calls captured as one HIP graph, replayed, HIP events",
+    }
+    if scatter:
+        sc_us = _graph_us_per_call(hp.scatter, L, reps)
+        sc_bytes = workloads.scatter_bytes(hp.n_computed, m.num_kv_heads, m.head_dim)
+        out["scatter"] = {"us_per_layer": round(sc_us, 2), "bytes": sc_bytes,
+                          "gbps": round(sc_bytes / (sc_us * 1e-6) / 1e9, 1),
+                          "frac_hbm_peak": round(sc_bytes / (sc_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+    if hp.n_reused:
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        rr_bytes = workloads.rerotate_bytes(hp.n_reused, L, m.num_kv_heads, m.head_dim, with_v=True)
+        rr_ms = _cold_ms(hp.rerotate, flush)
+        rr_dirty_ms = _cold_ms(hp.rerotate, flush, dirty=True)
+        out["rerotate"] = {"us_all_layers": round(rr_ms * 1e3, 1), "bytes": rr_bytes,
+                           "gbps": round(rr_bytes / (rr_ms * 1e-3) / 1e9, 1),
+                           "frac_hbm_peak": round(rr_bytes / (rr_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                           "dirty_mall_us": round(rr_dirty_ms * 1e3, 1),
+                           "timing": "cold: 512 MiB read (clean MALL) or write (dirty) before each run, median of 5"}
+        del flush
+    del hp
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_ttft(ratio: float, reps: int = 2):
     """Warm TTFT (ms) of the cold -> warm protocol of the reference's test_partial_recompute.py.
 
@@ -387,34 +462,65 @@ def run_decode(reps: int = 10):
     }
 
 
-def run_cpu_baseline(hp, budget_s: float = 20.0):
-    """The oracle (fp32 torch on the host CPU) on a bounded sample of the same workload."""
+def _cpu_median(fn, runs: int, budget_s: float):
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= runs:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def run_cpu_baseline(hp, budget_s: float = 12.0):
+    """The oracle (fp32 torch on the host CPU) on bounded samples of the same workload:
+    one layer's attention, the all-layer re-rotation + copy of the reused image KV, and
+    one layer's store_kvcache scatter (the reference's CPU-runnable restatements)."""
     from oracle import attention as oattn
+    from oracle import rope as orope
+    from oracle import scatter as oscat
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    m = hp.model
     kc = hp.k_caches[0].cpu()
     vc = hp.v_caches[0].cpu()
     q = hp.q.cpu()
     bt = hp.block_tables.cpu().tolist()
     cu_q, cu_k = hp.cu_q_host, hp.cu_k_host
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        oattn.varlen_attention(q, kc, vc, cu_q, cu_k, hp.scale, True, bt, 256)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
-            break
-    times.sort()
-    med = times[len(times) // 2]
+    at_s, at_n = _cpu_median(lambda: oattn.varlen_attention(q, kc, vc, cu_q, cu_k, hp.scale, True, bt, 256),
+                             5, budget_s)
+    kv = hp.kv_cache.cpu()
+    old, new = hp.old_slots.cpu(), hp.new_slots.cpu()
+    cs = orope.rerotation_cos_sin(hp.deltas, m.head_dim, m.rope_theta, list(m.mrope_section))
+    seg = hp.seg.cpu()
+    rr_s, rr_n = _cpu_median(lambda: orope.rerotate_copy_kv(kv, old, new, cs, seg), 3, budget_s)
+    del kv
+    k_rows = hp.k.cpu()
+    v_rows = hp.v.cpu().contiguous()
+    slots = hp.slot_mapping.cpu().numpy()
+    kcache, vcache = kc.view(torch.int16).numpy(), vc.view(torch.int16).numpy()
+    kn, vn = k_rows.view(torch.int16).numpy(), v_rows.view(torch.int16).numpy()
+    sc_s, sc_n = _cpu_median(lambda: oscat.store_kvcache(kn, vn, kcache, vcache, slots), 20, budget_s / 4)
+    from vlcache_amd import workloads
+
+    rr_bytes = workloads.rerotate_bytes(hp.n_reused, m.num_layers, m.num_kv_heads, m.head_dim, with_v=True)
+    sc_bytes = workloads.scatter_bytes(hp.n_computed, m.num_kv_heads, m.head_dim)
     return {
-        "value": med * 1e6,
+        "value": at_s * 1e6,
         "unit": "us/layer (attention)",
         "cores": cores,
         "kind": "port",
-        "sample": f"{len(times)} runs of one layer's attention of the same workload (fp32 SDPA oracle, "
-                  f"median), host CPU: {_cpu_model()}",
+        "sample": f"{at_n} runs of one layer's attention of the same workload (fp32 SDPA oracle, median); "
+                  f"re-rotation + copy: {rr_n} runs of all {m.num_layers} layers; scatter: {sc_n} runs of one "
+                  f"layer; host CPU: {_cpu_model()}",
+        "kernels": {
+            "rerotate_copy": {"us_all_layers": round(rr_s * 1e6, 1), "gbps": round(rr_bytes / rr_s / 1e9, 2)},
+            "scatter": {"us_per_layer": round(sc_s * 1e6, 1), "gbps": round(sc_bytes / sc_s / 1e9, 2)},
+        },
     }
 
 
@@ -427,6 +533,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ttft", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other workloads' sub-results")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run one plain device-to-device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -448,6 +555,11 @@ def main():
 
     r = run_gpu(args.steps, args.warmup, args.workload)
     decode = run_decode() if not args.no_decode else None
+    others = {}
+    if not args.no_configs:
+        for name, kw in (("cfg3", {"scatter": True}), ("cfg4", {}), ("cfg5", {})):
+            if name != args.workload:
+                others[name] = run_config(name, args.steps, 1, **kw)
     wl, hp = r["wl"], r["hp"]
     ttft = None
     if not args.no_ttft:
@@ -525,6 +637,7 @@ def main():
         },
         "ms_per_step_graph": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
         "warm_ttft": ttft,
+        "configs": others,
     }
     print(json.dumps(line), flush=True)
 
