@@ -627,32 +627,3 @@ def test_decode_small_pages_group7(dev):
     say("decode: page 32, 7 q heads per kv head, lengths 95, 96, 97, 4000; page 16 (16-key tiles)")
     _decode_case(dev, [95, 96, 97, 4000], 28, 4, seed=63, page=32)
     _decode_case(dev, [15, 16, 17, 900], 16, 2, seed=66, page=16)
-
-
-@pytest.mark.parametrize("subs,hq,hkv", [
-    ([(1183, 1183), (64, 10741)], 16, 2),                 # the 4K warm request's call
-    ([(118, 118), (275, 3030), (64, 13432)] * 2, 28, 4),  # two-image 7B requests
-    ([(1, 700), (17, 17), (45, 2000), (129, 5130)], 8, 1),
-])
-def test_attention_fused_merge_matches_combine_kernel(dev, subs, hq, hkv):
-    """Split partials merged inside the attention launch (its grid fits the device, so
-    it is launched cooperatively) give the same bits as the separate combine kernel;
-    the merge leaves its counters at zero and reports no stopped wait."""
-    say(f"attention: fused merge vs combine kernel, subs={subs} heads={hq}/{hkv}")
-    q, kc, vc, bt, cu_q, cu_k = _paged_case(29, hq, hkv, subs)
-    pf = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, True, dev)
-    pc = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, True, dev, fused_merge=False)
-    assert pf.num_combine > 0 and pf.num_items <= 2 * kernels._num_cus(dev), (pf.num_items, pf.num_combine)
-    print(f"plan items={pf.num_items} combines={pf.num_combine}", flush=True)
-    args = (q.to(dev), kc.to(dev), vc.to(dev), torch.tensor(cu_q, dtype=torch.int32, device=dev),
-            torch.tensor(cu_k, dtype=torch.int32, device=dev), 128 ** -0.5, True, bt.to(dev))
-    fused = [kernels.varlen_attention(*args, plan=pf).cpu() for _ in range(3)]
-    sep = kernels.varlen_attention(*args, plan=pc).cpu()
-    torch.cuda.synchronize()
-    assert pf.merge_status() == 0
-    off = (pf.num_slots * kernels.SLOT_BYTES + 255) // 256 * 256
-    assert int(pf.workspace[off:].count_nonzero()) == 0, "merge counters not back at zero"
-    for o in fused:
-        assert torch.equal(o.view(torch.int16), sep.view(torch.int16)), "fused merge != combine kernel"
-    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), 256)
-    assert_attn_close(fused[0], ref, what="fused merge")

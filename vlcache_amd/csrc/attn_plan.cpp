@@ -92,7 +92,7 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
     if (nsplit <= 1) {
       Item it{};
       it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;
-      it.v[4] = 0; it.v[5] = t.kmax; it.v[6] = -1; it.v[11] = -1;
+      it.v[4] = 0; it.v[5] = t.kmax; it.v[6] = -1;
       bounds(it.v, t.b);
       it.cost = std::max(t.nkt, 1);
       items.push_back(it);
@@ -104,7 +104,6 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
     c.v[0] = t.b; c.v[1] = t.g; c.v[2] = t.qs; c.v[3] = t.qc; c.v[4] = next_slot; c.v[5] = nsplit;
     bounds(c.v, t.b);
     c.cost = nsplit;
-    const int32_t comb_index = (int32_t)combines.size();
     combines.push_back(c);
     for (int s = 0; s < nsplit; ++s) {
       Item it{};
@@ -112,7 +111,6 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
       const int ke = std::min(t.kmax, (s + 1) * per * kTileK);
       it.v[0] = t.b; it.v[1] = t.g; it.v[2] = t.qs; it.v[3] = t.qc;
       it.v[4] = kb; it.v[5] = ke; it.v[6] = next_slot + s;
-      it.v[11] = comb_index; it.v[12] = s; it.v[13] = nsplit;
       bounds(it.v, t.b);
       it.cost = (ke - kb + kTileK - 1) / kTileK;
       items.push_back(it);
@@ -124,7 +122,7 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
 
   const int64_t need = kHeaderInts + (int64_t)(items.size() + combines.size()) * kItemInts;
   *plan_len = need;
-  *workspace_bytes = workspace_size(next_slot, (int64_t)combines.size());
+  *workspace_bytes = (int64_t)next_slot * kSlotBytes;
   if (!plan || plan_capacity < need) return VLC_ERR_CAPACITY;
   std::memset(plan, 0, sizeof(int32_t) * kHeaderInts);
   plan[kPMagic] = kPlanMagic;

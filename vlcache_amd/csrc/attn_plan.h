@@ -30,18 +30,12 @@ enum PlanField {
   kPNumHeadsKv = 8,
   kPCausal = 9,
   kPHeadDim = 10,
-  // 0: split partials are merged inside the attention launch when its grid fits the
-  // device at once (cooperative launch), else by the combine kernel; 1: always by the
-  // combine kernel.  vlc_attn_plan writes 0; a caller may set 1 in its host copy.
-  kPMergeMode = 11,
 };
 
 // Work item (int32 x 16): one workgroup.
 //   [0] seq  [1] kv_head  [2] q_start  [3] q_count  [4] k_begin  [5] k_end
 //   [6] partial slot (-1 = write the normalised output)
-//   [7] q0 = cu_seqlens_q[seq]  [8] sq  [9] k0 = cu_seqlens_k[seq]  [10] sk
-//   split items: [11] combine item (query tile) index  [12] split index  [13] splits of the tile
-//   [14..15] unused
+//   [7] q0 = cu_seqlens_q[seq]  [8] sq  [9] k0 = cu_seqlens_k[seq]  [10] sk  [11..15] unused
 // Combine item (int32 x 16): merges the partial slots of one query tile.
 //   [0] seq  [1] kv_head  [2] q_start  [3] q_count  [4] first slot  [5] num splits
 //   [7] q0  [8] sq  [9] k0  [10] sk  [6, 11..15] unused
@@ -49,13 +43,6 @@ enum PlanField {
 
 // Bytes of workspace per partial slot: bf16 O/l [kCols][kHeadDim] + fp32 (m, l) [kCols].
 constexpr int64_t kSlotBytes = (int64_t)kCols * kHeadDim * 2 + (int64_t)kCols * 2 * 4;
-
-// Workspace layout: part_o [slots][kCols][kHeadDim] bf16 | part_ml [slots][kCols][2] fp32 |
-// counters: status word, then (arrive, depart) u32 per combine item, zero between calls.
-inline int64_t counter_offset(int64_t n_slots) { return (n_slots * kSlotBytes + 255) & ~int64_t(255); }
-inline int64_t workspace_size(int64_t n_slots, int64_t n_combine) {
-  return n_combine > 0 ? counter_offset(n_slots) + 4 * (1 + 2 * n_combine) : n_slots * kSlotBytes;
-}
 
 }  // namespace attn
 }  // namespace vlc

@@ -27,9 +27,7 @@
 // product, O accumulated in fp32 and normalised once at the end.  Items whose
 // key range was split write their normalised O (bf16) with (m, l) to a
 // workspace slot; attn_combine merges the slots of a query tile.
-#include <mutex>
 #include <type_traits>
-#include <vector>
 
 #include "attn_plan.h"
 #include "common.h"
@@ -59,7 +57,6 @@ struct Params {
   uint16_t* out;
   uint16_t* part_o;  // [slots][kCols][kHeadDim] bf16: the split's own normalised output O_s / l_s
   float* part_ml;    // [slots][kCols][2] fp32: (m_s in scaled log2 units, l_s)
-  uint32_t* counters;  // fused merge: [0] status, then (arrive, depart) per query tile; else null
   int64_t q_row_stride;
   int64_t k_row_stride;
   int64_t v_row_stride;
@@ -174,34 +171,6 @@ __device__ __forceinline__ float half_wave_max(float x) {
   return fmaxf(a, b);
 }
 
-// ---- device-coherent accesses of the fused merge ---------------------------------
-// The split partials of a query tile are written by workgroups on different XCDs,
-// whose L2 caches are not coherent with each other.  They are stored and loaded
-// at device scope (sc1: through to memory, not served from a stale L2 line);
-// each writer waits for its stores to complete before it takes its ticket, and a
-// reader loads only after it has seen every ticket.
-__device__ __forceinline__ void st16_dev(void* addr, u32x4v v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(addr), "v"(v) : "memory");
-}
-__device__ __forceinline__ u32x4v ld16_dev(const void* addr) {
-  u32x4v v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(addr) : "memory");
-  return v;
-}
-__device__ __forceinline__ void st_ml_dev(float* addr, float m, float l) {
-  const uint64_t bits = (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(l) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(addr), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 ld_ml_dev(const float* addr) {
-  const uint64_t bits =
-      __hip_atomic_load(reinterpret_cast<const uint64_t*>(addr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
-}
-// Polls of a split's wait for the other splits of its query tile (each after an
-// s_sleep of ~128 cycles): ~0.5 s, far beyond any real wait.  A wait that runs
-// out sets bit 0 of the status word and skips the merge, so every wave exits.
-constexpr uint32_t kMaxMergePolls = 1u << 22;
-
 template <int MODE>
 __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_buf0[kTileK * 256];
@@ -209,7 +178,6 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   __shared__ __attribute__((aligned(1024))) uint8_t v_buf0[kTileK * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t v_buf1[kTileK * 256];
   __shared__ int32_t tile_blk[kMaxItemTiles];  // kPagedTiles: block id of each key tile
-  __shared__ int32_t merge_go;                 // fused merge: every split of the tile has landed
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -636,107 +604,13 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
       uint16_t* dst = slot < 0 ? p.out + (int64_t)(q0 + q_start + posx) * p.out_row_stride +
                                      (int64_t)(g * p.group + colx - posx * p.group) * kHeadDim
                                : p.part_o + ((int64_t)slot * kCols + colx) * kHeadDim;
-      if (slot >= 0 && p.counters)
-        st16_dev(dst + 8 * ch, v);
-      else
-        *reinterpret_cast<u32x4v*>(dst + 8 * ch) = v;
+      *reinterpret_cast<u32x4v*>(dst + 8 * ch) = v;
     }
   }
   if (slot >= 0 && valid && hf == 0) {
     float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
-    if (p.counters) {
-      st_ml_dev(ml, m_run, l_tot);
-    } else {
-      ml[0] = m_run;
-      ml[1] = l_tot;
-    }
-  }
-  if (slot < 0 || !p.counters) return;
-
-  // ---- fused merge (the launch made every workgroup resident) ----------------------
-  // Each split takes a ticket once its partial has landed, waits until the query
-  // tile's splits all have, then merges its share of the tile's columns with the
-  // arithmetic of attn_combine_kernel (max over the splits first, then the sum of
-  // 2^(m_s - M) l_s Ohat_s in split order), so both paths give the same bits.  The
-  // last split to leave resets the tile's counters for the next call.
-  const int comb = it[11], s_idx = it[12], nsplit = it[13];
-  uint32_t* arrive = p.counters + 1 + 2 * comb;
-  uint32_t* depart = arrive + 1;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
-  __syncthreads();
-  if (tid == 0) {
-    __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t polls = 0;
-    while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)nsplit &&
-           polls < kMaxMergePolls) {
-      __builtin_amdgcn_s_sleep(2);
-      ++polls;
-    }
-    const bool ok = polls < kMaxMergePolls;
-    if (!ok) __hip_atomic_fetch_or(p.counters, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_go = ok ? 1 : 0;
-  }
-  __syncthreads();
-  if (merge_go) {
-    const int ncol = q_count * p.group;  // valid columns of the tile
-    const int ca = (int)((int64_t)s_idx * ncol / nsplit);
-    const int cb = (int)((int64_t)(s_idx + 1) * ncol / nsplit);
-    const int first = slot - s_idx;
-    constexpr int kLanes = kHeadDim / 8;  // 16 lanes per column, 8 dims each
-    constexpr int kBatch = 16;
-    for (int u = tid; u < (cb - ca) * kLanes; u += kThreads) {
-      const int colx = ca + u / kLanes;
-      const int d = (u % kLanes) * 8;
-      const float* ml = p.part_ml + ((int64_t)first * kCols + colx) * 2;
-      const uint16_t* po = p.part_o + ((int64_t)first * kCols + colx) * kHeadDim + d;
-      const int64_t ml_stride = (int64_t)kCols * 2, po_stride = (int64_t)kCols * kHeadDim;
-      float mmax = -INFINITY;
-      for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
-        float2 mls[kBatch];
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) mls[k] = ld_ml_dev(ml + min(s0 + k, nsplit - 1) * ml_stride);
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) mmax = fmaxf(mmax, mls[k].x);
-      }
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      float lsum = 0.f;
-      if (mmax != -INFINITY) {
-        for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
-          float2 mls[kBatch];
-          u32x4v v[kBatch];
-#pragma unroll
-          for (int k = 0; k < kBatch; ++k) {
-            const int sx = min(s0 + k, nsplit - 1);
-            mls[k] = ld_ml_dev(ml + sx * ml_stride);
-            v[k] = ld16_dev(po + sx * po_stride);
-          }
-#pragma unroll
-          for (int k = 0; k < kBatch; ++k) {
-            const float wl = s0 + k < nsplit ? fast_exp2(mls[k].x - mmax) * mls[k].y : 0.f;
-            lsum += wl;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
-              acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
-            }
-          }
-        }
-      }
-      const int posx = colx / p.group;
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint16_t* orow = p.out + (int64_t)(q0 + q_start + posx) * p.out_row_stride +
-                       (int64_t)(g * p.group + colx - posx * p.group) * kHeadDim + d;
-      u32x4v w;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
-      *reinterpret_cast<u32x4v*>(orow) = w;
-    }
-  }
-  __syncthreads();  // every wave is past the wait before the counters can be reset
-  if (tid == 0 &&
-      __hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)nsplit - 1) {
-    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ml[0] = m_run;
+    ml[1] = l_tot;
   }
 }
 
@@ -822,46 +696,6 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) 
   *reinterpret_cast<u32x4v*>(orow) = w;
 }
 
-// Workgroups of attn_fwd_kernel<MODE> the current device holds at once (CUs x
-// resident workgroups per CU), cached per device; 0 when it cannot be queried.
-template <int MODE>
-int64_t resident_capacity() {
-  static std::mutex mu;
-  static int64_t cap[64] = {};
-  static bool known[64] = {};
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!known[dev]) {
-    int cus = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_fwd_kernel<MODE>, kThreads, 0) == hipSuccess)
-      cap[dev] = (int64_t)cus * per_cu;
-    known[dev] = true;
-  }
-  return cap[dev];
-}
-
-// Main kernel, then (unless the merge was fused into it) the combine kernel.
-template <int MODE>
-int launch_attention(Params prm, int64_t n_items, int64_t n_comb, bool allow_fused, hipStream_t s) {
-  if (n_comb > 0 && allow_fused && prm.counters && n_items <= resident_capacity<MODE>()) {
-    // Every workgroup resident at once (the split workgroups wait for each other).
-    void* args[] = {&prm};
-    if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(attn_fwd_kernel<MODE>), dim3((unsigned)n_items),
-                                   dim3(kThreads), args, 0, s) == hipSuccess)
-      return VLC_OK;
-    (void)hipGetLastError();  // not launched: take the two-kernel path
-  }
-  prm.counters = nullptr;
-  hipLaunchKernelGGL(attn_fwd_kernel<MODE>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
-  int st = launch_status();
-  if (st != VLC_OK || n_comb == 0) return st;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)n_comb, kCols / kCombineCols), dim3(kThreads), 0, s,
-                     prm);
-  return launch_status();
-}
-
 }  // namespace
 }  // namespace attn
 }  // namespace vlc
@@ -901,24 +735,6 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
       return VLC_ERR_PLAN;
     if (!is_item && (v[4] < 0 || v[5] < 1 || (int64_t)v[4] + v[5] > n_slots)) return VLC_ERR_PLAN;
   }
-  // Split items name their query tile's combine item, their index in it and its
-  // split count (the fused merge waits for that count and reads the tile's slots):
-  // each tile must have exactly its splits, in its own slots.
-  if (n_comb > 0) {
-    std::vector<int32_t> seen((size_t)n_comb, 0);
-    for (int64_t i = 0; i < n_items; ++i) {
-      const int32_t* v = h + kHeaderInts + i * kItemInts;
-      if (v[6] < 0) continue;
-      if (v[11] < 0 || v[11] >= n_comb) return VLC_ERR_PLAN;
-      const int32_t* c = h + kHeaderInts + (n_items + v[11]) * kItemInts;
-      if (v[12] < 0 || v[12] >= c[5] || v[13] != c[5] || v[6] != c[4] + v[12] || v[0] != c[0] || v[1] != c[1] ||
-          v[2] != c[2] || v[3] != c[3])
-        return VLC_ERR_PLAN;
-      ++seen[(size_t)v[11]];
-    }
-    for (int64_t ci = 0; ci < n_comb; ++ci)
-      if (seen[(size_t)ci] != h[kHeaderInts + (n_items + ci) * kItemInts + 5]) return VLC_ERR_PLAN;
-  }
   if (!q || !k || !v || !out) return VLC_ERR_INVALID;
   if (!(softmax_scale > 0.f)) return VLC_ERR_INVALID;
   // 16-byte vector access of every row.
@@ -929,8 +745,7 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
       k_row_stride < (int64_t)num_heads_kv * kHeadDim || v_row_stride < (int64_t)num_heads_kv * kHeadDim)
     return VLC_ERR_INVALID;
   if (block_table && (page_size <= 0 || bt_row_stride <= 0 || num_blocks <= 0)) return VLC_ERR_INVALID;
-  if (n_slots > 0 &&
-      (!workspace || workspace_bytes < workspace_size(n_slots, n_comb) || !aligned16(workspace)))
+  if (n_slots > 0 && (!workspace || workspace_bytes < n_slots * kSlotBytes || !aligned16(workspace)))
     return VLC_ERR_WORKSPACE;
 
   Params prm{};
@@ -947,9 +762,6 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   prm.part_ml = n_slots > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                                         n_slots * (int64_t)kCols * kHeadDim * 2)
                             : nullptr;
-  prm.counters = n_comb > 0 ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
-                                                          counter_offset(n_slots))
-                            : nullptr;
   prm.q_row_stride = q_row_stride;
   prm.k_row_stride = k_row_stride;
   prm.v_row_stride = v_row_stride;
@@ -962,9 +774,19 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   prm.scale_log2 = softmax_scale * 1.4426950408889634f;
 
   hipStream_t s = as_stream(stream);
-  const bool allow_fused = h[kPMergeMode] == 0;
   const int mode = !block_table ? kContiguous : (page_size % kTileK == 0 ? kPagedTiles : kPagedRows);
-  if (mode == kContiguous) return launch_attention<kContiguous>(prm, n_items, n_comb, allow_fused, s);
-  if (mode == kPagedTiles) return launch_attention<kPagedTiles>(prm, n_items, n_comb, allow_fused, s);
-  return launch_attention<kPagedRows>(prm, n_items, n_comb, allow_fused, s);
+  if (mode == kContiguous)
+    hipLaunchKernelGGL(attn_fwd_kernel<kContiguous>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  else if (mode == kPagedTiles)
+    hipLaunchKernelGGL(attn_fwd_kernel<kPagedTiles>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<kPagedRows>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  int st = launch_status();
+  if (st != VLC_OK) return st;
+  if (n_comb > 0) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)n_comb, kCols / kCombineCols), dim3(kThreads), 0,
+                       s, prm);
+    st = launch_status();
+  }
+  return st;
 }

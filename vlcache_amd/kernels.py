@@ -244,32 +244,10 @@ class AttnPlan:
     def num_slots(self) -> int:
         return int(self.host[3])
 
-    @property
-    def fused_merge(self) -> bool:
-        """Whether split partials may be merged inside the attention launch (header field 11)."""
-        return int(self.host[11]) == 0
-
-    def merge_status(self) -> int:
-        """The fused merge's status word (bit 0: a split stopped waiting for its tile's other
-        splits and skipped its merge).  Reads device memory: synchronises."""
-        if self.workspace is None or self.num_combine == 0:
-            return 0
-        off = (self.num_slots * SLOT_BYTES + 255) // 256 * 256
-        return int(self.workspace[off:off + 4].view(torch.int32).item())
-
-
-SLOT_BYTES = 128 * 128 * 2 + 128 * 2 * 4  # workspace bytes per split partial (bf16 O, fp32 (m, l))
-
 
 def plan_attention(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: int,
-                   head_dim: int, causal: bool, device, num_cus: int | None = None,
-                   fused_merge: bool = True) -> AttnPlan:
-    """Build the host work list (vlc_attn_plan) from HOST sequence boundaries.
-
-    fused_merge=False makes every call merge split partials with the separate
-    combine kernel; by default they are merged inside the attention launch when its
-    grid fits the device at once.  The workspace is allocated zeroed (its merge
-    counters must start at zero; every call leaves them so)."""
+                   head_dim: int, causal: bool, device, num_cus: int | None = None) -> AttnPlan:
+    """Build the host work list (vlc_attn_plan) from HOST sequence boundaries."""
     lib = _lib.load()
     cu_q = np.ascontiguousarray(np.asarray(cu_seqlens_q, dtype=np.int32))
     cu_k = np.ascontiguousarray(np.asarray(cu_seqlens_k, dtype=np.int32))
@@ -290,12 +268,10 @@ def plan_attention(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: i
     st = lib.vlc_attn_plan(*args, host.ctypes.data_as(ip), host.size, ctypes.byref(plan_len),
                            ctypes.byref(ws))
     _lib.check("vlc_attn_plan", st)
-    if not fused_merge:
-        host[11] = 1
     if device.type == "cuda":
         pinned = torch.from_numpy(host).pin_memory()
         dev = pinned.to(device, non_blocking=True)
-        workspace = torch.zeros(ws.value, dtype=torch.uint8, device=device) if ws.value > 0 else None
+        workspace = torch.empty(ws.value, dtype=torch.uint8, device=device) if ws.value > 0 else None
     else:
         dev = torch.from_numpy(host.copy())
         workspace = None
