@@ -96,9 +96,18 @@ def _check_plan_covers(cu_q, cu_k, hq, hkv, causal, num_cus):
             for a, c in zip(ranges, ranges[1:]):
                 assert a[1] == c[0]
     assert sorted(slots_seen) == list(range(int(plan.host[3])))
-    # longest-first order
+    # order: longest first, except a plan of one wave of workgroups (more items than CUs,
+    # at most two per CU), where workgroup c + k shares a CU with workgroup k: the c - m
+    # largest run alone (slots m .. c-1) and the others pair large with small
     cost = [max(1, -(-(int(i[5]) - int(i[4])) // 64)) for i in items]
-    assert cost == sorted(cost, reverse=True)
+    d = sorted(cost, reverse=True)
+    n, c = len(cost), max(1, num_cus)
+    if c < n <= 2 * c:
+        m = n - c
+        expect_cost = d[c - m:c] + d[:c - m] + d[c:][::-1]
+        assert cost == expect_cost
+    else:
+        assert cost == d
     return plan
 
 

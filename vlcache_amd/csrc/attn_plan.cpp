@@ -31,6 +31,26 @@ struct Item {
   int64_t cost;
 };
 
+// The dispatcher places the first num_cus workgroups of a launch one per CU and
+// workgroup num_cus + i next to workgroup i (measured on MI355X for a grid of two
+// resident workgroups per CU).  When every item fits in one such wave, pair them
+// so that CU loads even out: the largest items run alone, the rest pair a large
+// item with a small one.  `items` is sorted longest first; multi-wave plans keep
+// that order (each freed slot takes the next longest item).
+void pair_for_cus(std::vector<Item>& items, int num_cus) {
+  const int64_t n = (int64_t)items.size(), c = num_cus;
+  if (n <= c || n > 2 * c) return;
+  const int64_t m = n - c;  // items in second slots
+  std::vector<Item> out(items.size());
+  // first slots: [0, m) the paired ones (the smallest m of the c largest, largest
+  // first), [m, c) the c - m largest, alone on their CU
+  for (int64_t k = 0; k < m; ++k) out[k] = items[c - m + k];
+  for (int64_t j = 0; j < c - m; ++j) out[m + j] = items[j];
+  // second slot of first slot k: the k-th smallest of the remaining items
+  for (int64_t k = 0; k < m; ++k) out[c + k] = items[n - 1 - k];
+  items.swap(out);
+}
+
 }  // namespace
 
 VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num_seqs,
@@ -119,6 +139,7 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
   }
   std::stable_sort(items.begin(), items.end(),
                    [](const Item& a, const Item& b) { return a.cost > b.cost; });
+  pair_for_cus(items, num_cus);
 
   const int64_t need = kHeaderInts + (int64_t)(items.size() + combines.size()) * kItemInts;
   *plan_len = need;

@@ -244,6 +244,17 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   }
 
 
+  // The eight K and eight V operand offsets of a step, kept in registers across
+  // the tile loop (each is the lane's base offset XOR a constant).
+  uint32_t kofs[8], vofs[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) kofs[kk] = koff0 ^ (uint32_t)(kk << 5);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    vofs[2 * mb] = voff0 ^ ((uint32_t)mb << 6);
+    vofs[2 * mb + 1] = voff0 ^ (((uint32_t)mb << 6) | 32u | 2048u);
+  }
+
   // ---- tile loads: wave w fills rows 16w .. 16w+15, 4 rows per instruction -----
   // Lane i writes LDS slot i%16 of row 16w + 4j + i/16, so it loads that row's
   // chunk (i%16) ^ swz(row) = (i%16) ^ ((i/16) << 2) ^ j.
@@ -403,7 +414,6 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     constexpr int kAhead = 3;
     const int kt = k_begin + t * kTileK;
     const DmaSrc dk = dma_src(t + 2, kcol, kst), dv = dma_src(t, vcol, vst);
-    const uint32_t kof = opaque(koff0), vof = opaque(voff0);
     const uint32_t lr = opaque(lrow0), lcn = opaque(lchunk0);
     const int rel = min(limit, k_end - 1) - kt - 4 * hf;  // MASKED: keys past rel are masked
 
@@ -411,16 +421,15 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     auto read_op = [&](int j) __attribute__((always_inline)) {
       if (j < 16) {  // V^T operand: key block j >> 3, 16-key chunk (j >> 2) & 1, dim block j & 3
         const uint8_t* vr = v_rd + ((j >> 3) * 32 + 16 * ((j >> 2) & 1)) * 256;
-        const uint32_t mb = (uint32_t)(j & 3) << 6;
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ mb)));
+            (__attribute__((address_space(3))) s16x4*)(vr + vofs[2 * (j & 3)]));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ (mb | 32u | 2048u))));
+            (__attribute__((address_space(3))) s16x4*)(vr + vofs[2 * (j & 3) + 1]));
         const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         op[j] = __builtin_bit_cast(bf16x8, w);
       } else {  // K operand: head-dim step (j - 16) >> 1, key block (j - 16) & 1
         const int kk = (j - 16) >> 1, kb = (j - 16) & 1;
-        op[j] = *reinterpret_cast<const bf16x8*>(k_rd + kb * 32 * 256 + (kof ^ (uint32_t)(kk << 5)));
+        op[j] = *reinterpret_cast<const bf16x8*>(k_rd + kb * 32 * 256 + kofs[kk]);
       }
     };
     auto mfma_op = [&](int j) __attribute__((always_inline)) {
@@ -456,12 +465,13 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
       if (i + kAhead < 32) read_op(i + kAhead);
       mfma_op(i);
       if (MODE != kPagedRows) {
+        // row (< 64) x row stride (< 2^24 bytes, checked on the host): a 24-bit multiply-add
         if (i < 4) {
-          dma16(dk.base, min(lr + 4 * i, dk.last) * (uint32_t)kst + ((lcn ^ (uint32_t)i) << 4),
+          dma16(dk.base, __umul24(min(lr + 4 * i, dk.last), (uint32_t)kst) + ((lcn ^ (uint32_t)i) << 4),
                 lds_u32(k_ld + (16 * wave + 4 * i) * 256));
         } else if (i < 8) {
           const int r = i - 4;
-          dma16(dv.base, min(lr + 4 * r, dv.last) * (uint32_t)vst + ((lcn ^ (uint32_t)r) << 4),
+          dma16(dv.base, __umul24(min(lr + 4 * r, dv.last), (uint32_t)vst) + ((lcn ^ (uint32_t)r) << 4),
                 lds_u32(v_ld + (16 * wave + 4 * r) * 256));
         }
       } else {
@@ -642,6 +652,52 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) 
   // weighted 0) so that a batch is in flight at once.
   constexpr int kLanes = kHeadDim / 8;  // lanes per column
   constexpr int kBatch = 16;
+  if (nsplit <= 32) {
+    // Up to 32 splits: every (m, l) and O load of the lane's column in flight at
+    // once (one memory round trip), then the max, then the sum in split order.
+    if (!valid) return;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    auto merge_once = [&](auto batch) __attribute__((always_inline)) {
+      constexpr int B = decltype(batch)::value;
+      float2 mls[B];
+      u32x4v v[B];
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const int sx = min(k, nsplit - 1);
+        mls[k] = *reinterpret_cast<const float2*>(ml + sx * ml_stride);
+        v[k] = *reinterpret_cast<const u32x4v*>(po + sx * po_stride);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < B; ++k)
+        if (k < nsplit) mx = fmaxf(mx, mls[k].x);
+      if (mx == -INFINITY) return;
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const float wl = k < nsplit ? fast_exp2(mls[k].x - mx) * mls[k].y : 0.f;
+        lsum += wl;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
+          acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
+        }
+      }
+    };
+    if (nsplit <= 4) merge_once(std::integral_constant<int, 4>{});
+    else if (nsplit <= 8) merge_once(std::integral_constant<int, 8>{});
+    else if (nsplit <= 16) merge_once(std::integral_constant<int, 16>{});
+    else merge_once(std::integral_constant<int, 32>{});
+    const int hh = col - pos * p.group;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
+                     (int64_t)(g * p.group + hh) * kHeadDim + d;
+    u32x4v w;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
+    *reinterpret_cast<u32x4v*>(orow) = w;
+    return;
+  }
   float mmax = -INFINITY;
   if (valid) {
     for (int s0 = 0; s0 < nsplit; s0 += 4 * kLanes) {
@@ -741,6 +797,8 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || q_row_stride % 8 ||
       k_row_stride % 8 || v_row_stride % 8 || out_row_stride % 8)
     return VLC_ERR_INVALID;
+  // tile-load offsets are 24-bit products: row (< 64) x row stride in bytes
+  if (k_row_stride * 2 >= (int64_t(1) << 24) || v_row_stride * 2 >= (int64_t(1) << 24)) return VLC_ERR_UNSUPPORTED;
   if (q_row_stride < (int64_t)num_heads_q * kHeadDim || out_row_stride < (int64_t)num_heads_q * kHeadDim ||
       k_row_stride < (int64_t)num_heads_kv * kHeadDim || v_row_stride < (int64_t)num_heads_kv * kHeadDim)
     return VLC_ERR_INVALID;
