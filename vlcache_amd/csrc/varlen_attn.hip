@@ -652,52 +652,6 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) 
   // weighted 0) so that a batch is in flight at once.
   constexpr int kLanes = kHeadDim / 8;  // lanes per column
   constexpr int kBatch = 16;
-  if (nsplit <= 32) {
-    // Up to 32 splits: every (m, l) and O load of the lane's column in flight at
-    // once (one memory round trip), then the max, then the sum in split order.
-    if (!valid) return;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    auto merge_once = [&](auto batch) __attribute__((always_inline)) {
-      constexpr int B = decltype(batch)::value;
-      float2 mls[B];
-      u32x4v v[B];
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        const int sx = min(k, nsplit - 1);
-        mls[k] = *reinterpret_cast<const float2*>(ml + sx * ml_stride);
-        v[k] = *reinterpret_cast<const u32x4v*>(po + sx * po_stride);
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int k = 0; k < B; ++k)
-        if (k < nsplit) mx = fmaxf(mx, mls[k].x);
-      if (mx == -INFINITY) return;
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        const float wl = k < nsplit ? fast_exp2(mls[k].x - mx) * mls[k].y : 0.f;
-        lsum += wl;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
-          acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
-        }
-      }
-    };
-    if (nsplit <= 4) merge_once(std::integral_constant<int, 4>{});
-    else if (nsplit <= 8) merge_once(std::integral_constant<int, 8>{});
-    else if (nsplit <= 16) merge_once(std::integral_constant<int, 16>{});
-    else merge_once(std::integral_constant<int, 32>{});
-    const int hh = col - pos * p.group;
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
-                     (int64_t)(g * p.group + hh) * kHeadDim + d;
-    u32x4v w;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
-    *reinterpret_cast<u32x4v*>(orow) = w;
-    return;
-  }
   float mmax = -INFINITY;
   if (valid) {
     for (int s0 = 0; s0 < nsplit; s0 += 4 * kLanes) {
