@@ -262,6 +262,33 @@ int vlc_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_c
                             int head_dim, float softmax_scale, int key_chunk, int grid_splits, int pipeline,
                             void* out, int64_t out_row_stride, void* stream);
 
+/*
+ * Vision tower: 2-D rotary embedding of q and k fused with the split of the QKV
+ * projection into zero-padded head rows for vlc_varlen_attn_fwd.
+ * Replaces qkv.split + reshape + apply_rotary_pos_emb_vision of q and k in
+ * VisionAttention.forward (models/qwen2_5_vl.py:176-199).
+ *
+ * qkv: [num_tokens, 3 * num_heads * head_dim] bf16 at row stride qkv_row_stride
+ *   (q heads, then k heads, then v heads; the checkpoint's packed layout).
+ * pos_hw: int32 [num_tokens][2], (patch row, patch column) of each token.
+ * cos_table / sin_table: bf16 [max_pos][head_dim / 4]; row p holds cos / sin of
+ *   the angle p * inv_freq[i] (the reference rounds the angle to bf16 before
+ *   taking cos / sin, models/qwen2_5_vl.py:486).  Dim j of a head, with
+ *   a = j mod head_dim/2, uses column a of row pos_h for a < head_dim/4 and
+ *   column a - head_dim/4 of row pos_w otherwise.  Positions are clamped to
+ *   [0, max_pos).
+ * y[j] = bf16(bf16(x[j]*cos) + bf16(rotate_half(x)[j]*sin)) for q and k, as the
+ *   reference's bf16 tensor arithmetic rounds; v is copied.
+ * out: [num_tokens][3][num_heads][padded_dim] bf16 at row stride out_row_stride;
+ *   dims head_dim..padded_dim-1 of every head are written as zero.
+ * head_dim % 16 == 0, padded_dim % 8 == 0, padded_dim >= head_dim; qkv, out and
+ * their row strides 16-byte aligned.
+ */
+int vlc_vision_rope_pad(const void* qkv, int64_t qkv_row_stride, const int32_t* pos_hw,
+                        const void* cos_table, const void* sin_table, int64_t max_pos,
+                        int64_t num_tokens, int num_heads, int head_dim, int padded_dim,
+                        void* out, int64_t out_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,14 @@ oracle's own formula):
                 for sq == sk, and layout invariances (paged == contiguous, block
                 permutation, GQA == MHA with repeated heads).
 
+* ``engine``    block pool and step scheduler (text-only).  Pinned by known-answer
+                step traces and invariants (tests/test_engine_host.py).
+* ``vision``    the vision tower in fp32: window layout, 2-D rotary (with the
+                reference's bf16 angles), blocks, merger.  Pinned against
+                transformers' Qwen2.5-VL vision tower and layout helpers, a
+                hand-derived window layout and a bit-level bf16 rounding
+                (tests/test_oracle_vision.py).
+
 The attention arithmetic of the reference lives in the external flash-attn
 library (pyproject.toml:18, no version pin, absent here): its exact bf16
 rounding is not reproducible, so attention parity is tolerance-based.

@@ -1,0 +1,222 @@
+"""GPU parity of the vision tower (models/qwen2_5_vl.py:93-531) against the CPU oracle.
+
+* vlc_vision_rope_pad: bit for bit against the oracle's bf16 rotation (given the
+  same cos/sin tables), v copied, padding zero; the device cos/sin tables within
+  one bf16 ulp of the oracle's (torch's cos/sin on host and device may round a
+  near-tie differently);
+* window and whole-image attention through the padded 128-dim heads against
+  the fp32 oracle under the per-(row, head) bar, including every row of a
+  4K image's whole-image attention sampled at full size;
+* the whole tower against the fp32 oracle (with the reference's bf16 angles) on
+  a tiny configuration and on the public 32-block configuration with small
+  images; the bf16 product and the fp32 oracle differ by bf16 rounding through
+  the blocks, so the bar is a per-row cosine (stated in each test);
+* the engine: a cold request runs the tower and fills the encoder cache, a warm
+  request reads it back and reports no vision time.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oattn
+from oracle import vision as ov
+from tests._util import assert_attn_close, row_cosines, say
+from vlcache_amd import kernels
+from vlcache_amd.vision import VisionLayout, VisionTransformer, vision_config
+
+pytestmark = pytest.mark.gpu
+
+REAL = dict(depth=32, hidden_size=1280, intermediate_size=3420, num_heads=16, out_hidden_size=2048, patch_size=14,
+            spatial_merge_size=2, temporal_patch_size=2, window_size=112, fullatt_block_indexes=[7, 15, 23, 31],
+            in_channels=3, hidden_act="silu")
+TINY = dict(REAL, depth=3, hidden_size=64, intermediate_size=96, num_heads=4, out_hidden_size=48,
+            fullatt_block_indexes=[1])
+
+
+def _tower(cfg: dict, params: dict, dev) -> VisionTransformer:
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            vt = VisionTransformer(vision_config(cfg, cfg["out_hidden_size"]))
+    finally:
+        torch.set_default_dtype(prev)
+    vt.load_checkpoint_weights({k: v.to(torch.bfloat16) for k, v in params.items()})
+    return vt.eval()
+
+
+def _pixels(grids, seed):
+    n = sum(t * h * w for t, h, w in grids)
+    return torch.randn(n, 3 * 2 * 14 * 14, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
+
+
+def _rope_inputs(dev, grids, heads=16, hd=80, seed=0):
+    lay = VisionLayout(grids, 112, 2, 14)
+    n = lay.num_patches
+    qkv = (torch.randn(n, 3 * heads * hd, generator=torch.Generator().manual_seed(seed))).to(torch.bfloat16)
+    with torch.device(dev):
+        vt = VisionTransformer(vision_config(dict(TINY, hidden_size=heads * hd, num_heads=heads), 48))
+    cos, sin = vt.rope_tables(lay.max_pos)
+    return lay, qkv, cos, sin
+
+
+def test_rope_tables_match_oracle(dev):
+    say("vision: bf16 cos/sin tables for positions 0..273")
+    _, _, cos, sin = _rope_inputs(dev, [(1, 154, 274)])
+    pos = np.stack([np.arange(274), np.zeros(274, np.int64)], -1)
+    ang = ov.rotary_angles(pos, 80, bf16_angles=True)[:, :20]
+    for got, ref in ((cos, ang.cos()), (sin, ang.sin())):
+        ref16 = ref.to(torch.bfloat16)
+        diff = (got.cpu().view(torch.int16).int() - ref16.view(torch.int16).int()).abs()
+        assert int(diff.max()) <= 1, "cos/sin tables differ by more than one bf16 ulp"
+
+
+@pytest.mark.parametrize("grids", [[(1, 16, 16)], [(1, 4, 4), (1, 20, 34), (2, 6, 10)], [(1, 154, 274)]],
+                         ids=["16x16", "three", "4k"])
+def test_vision_rope_pad_bit_exact(dev, grids):
+    say(f"vision: vlc_vision_rope_pad grids={grids}")
+    lay, qkv, cos, sin = _rope_inputs(dev, grids, seed=len(grids))
+    out = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
+    torch.cuda.synchronize()
+    out = out.cpu()
+    n = lay.num_patches
+    # The oracle's rotation with cos/sin per token gathered from the same tables.
+    ph, pw = torch.from_numpy(lay.pos_hw[:, 0]).long(), torch.from_numpy(lay.pos_hw[:, 1]).long()
+    c, s = cos.cpu(), sin.cpu()
+    c40, s40 = torch.cat((c[ph], c[pw]), -1), torch.cat((s[ph], s[pw]), -1)
+    c80, s80 = torch.cat((c40, c40), -1), torch.cat((s40, s40), -1)
+    q, k, v = qkv.reshape(n, 3, 16, 80).unbind(1)
+    for part, ref in ((0, ov.rope_bf16(q, c80, s80)), (1, ov.rope_bf16(k, c80, s80)), (2, v)):
+        assert torch.equal(out[:, part, :, :80].view(torch.int16), ref.view(torch.int16)), f"part {part}"
+    assert not out[:, :, :, 80:].view(torch.int16).any(), "padding must be zero"
+
+
+def test_vision_rope_pad_refuses_bad_tables(dev):
+    lay, qkv, cos, sin = _rope_inputs(dev, [(1, 16, 16)])
+    with pytest.raises(ValueError):
+        kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos[:, :10].contiguous(),
+                                sin[:, :10].contiguous(), 16, 80)
+
+
+@pytest.mark.parametrize("full", [False, True], ids=["windows", "whole-image"])
+def test_padded_attention(dev, full):
+    grids = [(1, 4, 4), (1, 20, 34), (2, 6, 10)]
+    say(f"vision: padded 80-dim attention, full={full}, grids={grids}")
+    lay, qkv, cos, sin = _rope_inputs(dev, grids, seed=7)
+    heads = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
+    cu = lay.cu_full if full else lay.cu_window
+    plan = kernels.plan_attention(cu, cu, 16, 16, 128, False, dev)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    o = kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu_t, cu_t, 80 ** -0.5, causal=False,
+                                 plan=plan).cpu()
+    hc = heads.cpu()
+    ref = oattn.varlen_attention(hc[:, 0, :, :80], hc[:, 1, :, :80], hc[:, 2, :, :80], cu, cu, 80 ** -0.5, False)
+    assert_attn_close(o[..., :80], ref, what="padded vision attention")
+    assert not o[..., 80:].view(torch.int16).any()
+
+
+def test_whole_image_attention_4k_sampled_rows(dev):
+    """Whole-image attention over a 4K image's 42196 patches at full size; 96 query rows
+    (spread over the sequence, both ends included) against the fp32 oracle."""
+    grids = [(1, 154, 274)]
+    say("vision: 4K whole-image attention, 42196 x 42196, non-causal")
+    lay, qkv, cos, sin = _rope_inputs(dev, grids, seed=11)
+    heads = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
+    cu = lay.cu_full
+    plan = kernels.plan_attention(cu, cu, 16, 16, 128, False, dev)
+    print(f"plan: items={plan.num_items} combines={plan.num_combine}", flush=True)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    o = kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu_t, cu_t, 80 ** -0.5, causal=False,
+                                 plan=plan).cpu()
+    hc = heads.cpu()
+    n = lay.num_patches
+    rows = torch.unique(torch.cat([torch.tensor([0, 1, n - 2, n - 1]), torch.linspace(0, n - 1, 92).long()]))
+    q = hc[rows, 0, :, :80].float()
+    k, v = hc[:, 1, :, :80].float(), hc[:, 2, :, :80].float()
+    s = torch.einsum("rhd,nhd->hrn", q, k) * 80 ** -0.5
+    ref = torch.einsum("hrn,nhd->rhd", torch.softmax(s, dim=-1), v)
+    assert_attn_close(o[rows, :, :80], ref, what="4K whole-image attention rows")
+    assert np.isfinite(o.float().numpy()).all()
+
+
+def _tower_check(dev, cfg, grids, seed, row_cos_min):
+    params = ov.random_params(cfg, seed=seed)
+    pix = _pixels(grids, seed + 1)
+    vt = _tower(cfg, params, dev)
+    got = vt(pix.to(dev), grids).float().cpu()
+    ref = ov.vision_forward(params, pix.float(), grids, cfg, bf16_angles=True)
+    cos, _, _ = row_cosines(got, ref)
+    worst = float(cos.min())
+    rel = float((got - ref).norm() / ref.norm())
+    print(f"rows={got.shape[0]} worst row cosine {worst:.6f}, relative L2 error {rel:.2e}", flush=True)
+    assert got.shape == ref.shape
+    assert worst >= row_cos_min, f"worst row cosine {worst:.6f} < {row_cos_min}"
+    return vt, pix, got
+
+
+def test_tower_tiny_config(dev):
+    """3 blocks (one whole-image), hidden 64, 4 heads of 16 dims; bar: every output row's
+    cosine with the fp32 oracle >= 0.9995."""
+    grids = [(1, 8, 12), (1, 4, 6), (1, 18, 30)]
+    say(f"vision tower, tiny config, grids={grids}")
+    _tower_check(dev, TINY, grids, 3, 0.9995)
+
+
+def test_tower_public_config_small_images(dev):
+    """The public configuration (32 blocks of hidden 1280, 16 heads of 80 dims, whole-image
+    attention at blocks 7/15/23/31) on two small images; bar: every output row's cosine
+    with the fp32 oracle >= 0.999 (bf16 activations and weights through 32 blocks)."""
+    grids = [(1, 16, 16), (1, 20, 34)]
+    say(f"vision tower, public config, grids={grids}")
+    _tower_check(dev, REAL, grids, 5, 0.999)
+
+
+def test_tower_batch_equals_single_images(dev):
+    """Images batched into one call give each image's own embeddings (windows and whole-image
+    sequences never cross images); GEMMs may round differently at another row count, so
+    the bar is the per-row cosine >= 0.9999."""
+    grids = [(1, 8, 12), (1, 18, 30)]
+    say("vision tower: batch of two == each alone")
+    params = ov.random_params(TINY, seed=9)
+    vt = _tower(TINY, params, dev)
+    pix = _pixels(grids, 10).to(dev)
+    both = vt(pix, grids).float().cpu()
+    a = vt(pix[:96], grids[:1]).float().cpu()
+    b = vt(pix[96:], grids[1:]).float().cpu()
+    cos, _, _ = row_cosines(both, torch.cat([a, b]))
+    assert float(cos.min()) >= 0.9999
+
+
+def test_engine_runs_the_tower_on_a_cold_image(dev):
+    """Cold request: the tower runs (vit_time > 0) and its embeddings enter the encoder
+    cache; they equal a direct call of the tower bit for bit.  Warm request with the
+    same image: a cache hit, no vision time."""
+    from vlcache_amd import LLM, SamplingParams
+
+    text = dict(architectures=["Qwen2_5_VLForConditionalGeneration"], hidden_size=256, intermediate_size=512,
+                num_hidden_layers=2, num_attention_heads=2, num_key_value_heads=1, head_dim=128,
+                vocab_size=151936, rms_norm_eps=1e-6, rope_theta=1e6,
+                rope_scaling={"type": "mrope", "mrope_section": [16, 24, 24]}, max_position_embeddings=8192,
+                tie_word_embeddings=True, image_token_id=151655, eos_token_id=151645,
+                vision_config=dict(TINY, out_hidden_size=256))
+    say("engine with a vision tower: cold then warm request")
+    llm = LLM(text, recompute_ratio=0.1, num_kvcache_blocks=16, max_model_len=4096, enforce_eager=True)
+    grid = (1, 20, 34)
+    n_img = 10 * 17
+    pix = _pixels([grid], 21)
+    rng = np.random.default_rng(0)
+    toks = lambda p, s: ([int(x) for x in rng.integers(1, 150000, p)] + [151655] * n_img +  # noqa: E731
+                         [int(x) for x in rng.integers(1, 150000, s)])
+    mm = {"pixel_values": pix, "image_grid_thw": torch.tensor([list(grid)])}
+    sp = SamplingParams(temperature=0.6, max_tokens=1)
+    cold = llm.generate([toks(40, 16)], sp, mm_inputs=[mm])[0]
+    runner = llm.model_runner
+    cache = runner.encoder_cache
+    assert len(cache) == 1 and cold["vit_time"] > 0
+    h = next(iter(cache._entries))
+    direct = runner.model.visual(pix.to(dev), [grid])
+    assert torch.equal(cache.get(h).view(torch.int16), direct.view(torch.int16))
+    warm = llm.generate([toks(128, 16)], sp, mm_inputs=[mm])[0]
+    assert warm["vit_time"] == 0.0 and cache.hits >= 2

@@ -14,7 +14,11 @@ from types import SimpleNamespace
 
 import torch
 
-# Public Qwen2.5-VL-3B-Instruct text-tower shapes.
+# Public Qwen2.5-VL vision_config (both sizes; out_hidden_size is the text hidden size).
+QWEN25_VL_VISION = dict(depth=32, hidden_size=1280, intermediate_size=3420, num_heads=16, in_channels=3,
+                        patch_size=14, temporal_patch_size=2, spatial_merge_size=2, window_size=112,
+                        fullatt_block_indexes=[7, 15, 23, 31], hidden_act="silu", tokens_per_second=2)
+# Public Qwen2.5-VL-3B-Instruct shapes.
 QWEN25_VL_3B = dict(
     architectures=["Qwen2_5_VLForConditionalGeneration"],
     hidden_size=2048, intermediate_size=11008, num_hidden_layers=36, num_attention_heads=16,
@@ -22,10 +26,12 @@ QWEN25_VL_3B = dict(
     rope_scaling={"type": "mrope", "mrope_section": [16, 24, 24]}, max_position_embeddings=128000,
     tie_word_embeddings=True, image_token_id=151655, vision_start_token_id=151652, eos_token_id=151645,
     spatial_merge_size=2, torch_dtype="bfloat16",
+    vision_config=dict(QWEN25_VL_VISION, out_hidden_size=2048),
 )
-# Public Qwen2.5-VL-7B-Instruct text-tower shapes.
+# Public Qwen2.5-VL-7B-Instruct shapes.
 QWEN25_VL_7B = dict(QWEN25_VL_3B, hidden_size=3584, intermediate_size=18944, num_hidden_layers=28,
-                    num_attention_heads=28, num_key_value_heads=4, vocab_size=152064, tie_word_embeddings=False)
+                    num_attention_heads=28, num_key_value_heads=4, vocab_size=152064, tie_word_embeddings=False,
+                    vision_config=dict(QWEN25_VL_VISION, out_hidden_size=3584))
 
 _DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
 

@@ -1,0 +1,118 @@
+// 2-D rotary embedding of the vision tower's q and k, fused with the split of the
+// QKV projection into head rows padded for the attention kernel.
+//
+// Replaces, per vision block, qkv.split + reshape + apply_rotary_pos_emb_vision
+// of q and k (models/qwen2_5_vl.py:176-199).  The reference's cos/sin and q/k are
+// bf16 tensors there, so every product and the sum round to bf16:
+//   y[j] = bf16( bf16(x[j] * cos[j]) + bf16(r[j] * sin[j]) ),
+//   r[j] = -x[j + D/2] for j < D/2, x[j - D/2] otherwise (rotate_half),
+// where an fp32 product of two bf16 values is exact, so each term rounds once,
+// and the sum is an fp32 add rounded to bf16: the same bits as the reference's
+// three elementwise bf16 ops.  cos[j]/sin[j] of dim j come from the caller's
+// bf16 tables [max_pos][D/4]: with a = j mod D/2, frequency a of the row axis
+// (table row = patch row) for a < D/4, frequency a - D/4 of the column axis
+// (table row = patch column) otherwise (the reference's cat(rpe, rpe) of the
+// [h-axis | w-axis] angles, :452-462, :486-487).
+//
+// Output: [n][3][num_heads][padded_dim] bf16 (q, k, v), dims head_dim.. of each
+// head zero, so the attention kernel (128-dim heads) computes the 80-dim
+// attention exactly: zero dims add nothing to q.k, and the padded output dims
+// are zero.  v is copied bit for bit.
+//
+// Work: one lane per 16-byte output chunk; lanes of a head row are adjacent, so
+// loads and stores coalesce.  A rotated chunk also reads the partner chunk D/2
+// away in the same head (L1/L2 hit: the same 160-byte head row).
+#include "common.h"
+
+namespace vlc {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+__global__ __launch_bounds__(kThreads) void vision_rope_pad_kernel(
+    const char* __restrict__ qkv, int64_t qkv_stride_b, const int32_t* __restrict__ pos_hw,
+    const uint16_t* __restrict__ cos_tab, const uint16_t* __restrict__ sin_tab, int max_pos,
+    uint32_t total, int num_heads, int head_dim, int chunks_per_head, char* __restrict__ out,
+    int64_t out_stride_b) {
+  const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+  if (u >= total) return;
+  const int heads3 = 3 * num_heads;
+  const uint32_t rest = u / (uint32_t)chunks_per_head;
+  const int c = (int)(u - rest * (uint32_t)chunks_per_head);
+  const uint32_t n = rest / (uint32_t)heads3;
+  const int hp = (int)(rest - n * (uint32_t)heads3);  // part * num_heads + head
+  u32x4* dst = reinterpret_cast<u32x4*>(out + (int64_t)n * out_stride_b +
+                                        ((int64_t)hp * chunks_per_head + c) * 16);
+  const int d0 = c * 8;
+  if (d0 >= head_dim) {
+    *dst = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const char* row = qkv + (int64_t)n * qkv_stride_b + (int64_t)hp * head_dim * 2;
+  const u32x4 xv = *reinterpret_cast<const u32x4*>(row + d0 * 2);
+  if (hp >= 2 * num_heads) {  // v
+    *dst = xv;
+    return;
+  }
+  const int half = head_dim >> 1, quarter = head_dim >> 2;
+  const bool lo = d0 < half;
+  const u32x4 pv = *reinterpret_cast<const u32x4*>(row + (lo ? d0 + half : d0 - half) * 2);
+  int ph = pos_hw[2 * n], pw = pos_hw[2 * n + 1];
+  ph = ph < 0 ? 0 : (ph >= max_pos ? max_pos - 1 : ph);
+  pw = pw < 0 ? 0 : (pw >= max_pos ? max_pos - 1 : pw);
+  const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+  const uint32_t ps[4] = {pv.x, pv.y, pv.z, pv.w};
+  uint32_t ys[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = d0 + 2 * w + h;
+      const int a = lo ? j : j - half;
+      const int t = a < quarter ? ph * quarter + a : pw * quarter + (a - quarter);
+      const float cs = bf16_bits_to_f32(cos_tab[t]);
+      const float sn = bf16_bits_to_f32(sin_tab[t]);
+      const float x = bf16_bits_to_f32((xs[w] >> (16 * h)) & 0xffffu);
+      const float p = bf16_bits_to_f32((ps[w] >> (16 * h)) & 0xffffu);
+      const float r = lo ? -p : p;
+      const float y = rbf(x * cs) + rbf(r * sn);
+      packed |= f32_to_bf16_bits(y) << (16 * h);
+    }
+    ys[w] = packed;
+  }
+  *dst = u32x4{ys[0], ys[1], ys[2], ys[3]};
+}
+
+}  // namespace
+}  // namespace vlc
+
+VLC_API int vlc_vision_rope_pad(const void* qkv, int64_t qkv_row_stride, const int32_t* pos_hw,
+                                const void* cos_table, const void* sin_table, int64_t max_pos,
+                                int64_t num_tokens, int num_heads, int head_dim, int padded_dim,
+                                void* out, int64_t out_row_stride, void* stream) {
+  using namespace vlc;
+  if (num_tokens < 0 || num_heads <= 0 || head_dim <= 0 || head_dim % 16 != 0 ||
+      padded_dim < head_dim || padded_dim % 8 != 0 || max_pos <= 0 || max_pos >= (1 << 24))
+    return VLC_ERR_INVALID;
+  if (qkv_row_stride < 3 * (int64_t)num_heads * head_dim ||
+      out_row_stride < 3 * (int64_t)num_heads * padded_dim)
+    return VLC_ERR_INVALID;
+  if (num_tokens == 0) return VLC_OK;
+  if (!qkv || !pos_hw || !cos_table || !sin_table || !out) return VLC_ERR_INVALID;
+  if (!aligned16(qkv) || !aligned16(out) || (qkv_row_stride * 2) % 16 != 0 || (out_row_stride * 2) % 16 != 0)
+    return VLC_ERR_UNSUPPORTED;
+  if ((int64_t)(head_dim / 4) * max_pos >= ((int64_t)1 << 31)) return VLC_ERR_UNSUPPORTED;
+  const int cph = padded_dim / 8;
+  const int64_t total = num_tokens * 3 * num_heads * (int64_t)cph;
+  if (total >= ((int64_t)1 << 32)) return VLC_ERR_UNSUPPORTED;  // 32-bit chunk index
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(vision_rope_pad_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream),
+                     static_cast<const char*>(qkv), qkv_row_stride * 2, pos_hw,
+                     static_cast<const uint16_t*>(cos_table), static_cast<const uint16_t*>(sin_table),
+                     (int)max_pos, (uint32_t)total, num_heads, head_dim, cph, static_cast<char*>(out),
+                     out_row_stride * 2);
+  return launch_status();
+}

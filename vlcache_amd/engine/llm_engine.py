@@ -30,7 +30,8 @@ from .sequence import Sequence
 def image_hash(pixel_values: torch.Tensor, grid_thw: torch.Tensor) -> int:
     h = xxhash.xxh64()
     h.update(grid_thw.cpu().numpy().tobytes())
-    h.update(pixel_values.cpu().numpy().tobytes())
+    # raw bytes of any dtype (numpy has no bf16): the same bytes as numpy's tobytes() for fp32
+    h.update(pixel_values.detach().cpu().contiguous().view(torch.uint8).numpy().tobytes())
     return h.intdigest()
 
 

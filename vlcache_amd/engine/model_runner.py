@@ -13,14 +13,18 @@ prepare_sample, run_model, run, allocate_kv_cache, exit.  Differences:
     use_mrope is set, else the reference's 1-D positions;
   * host preparation is vectorised (numpy) instead of per-token Python loops;
   * visual embeddings come from a bounded encoder cache (engine/encoder_cache.py)
-    sized by encoder_cache_ratio; the vision tower is not part of this path, so a
-    miss takes the caller's image_embeds, or seeded synthetic embeddings only when
-    the config opts in (synthetic_vision), and raises otherwise;
+    sized by encoder_cache_ratio; the images that miss it take the caller's
+    image_embeds when given, else run through the vision tower in one batch (an
+    image repeated in the batch runs once); a miss with neither pixel_values nor
+    a vision tower uses seeded synthetic embeddings only when the config opts in
+    (synthetic_vision), and raises otherwise;
   * every decode plan shares one workspace sized once for max_num_seqs requests
     of up to max_model_len tokens;
   * no tensor parallelism, no shared-memory RPC: one process, one GPU.
 """
 from __future__ import annotations
+
+from time import perf_counter
 
 import numpy as np
 import torch
@@ -161,7 +165,7 @@ class ModelRunner:
         logit_indices = []
         vidx = 0
         has_partial = False
-        mm = {"image_hashes": [], "image_grid_thw": [], "image_embeds": [], "recompute": []}
+        mm = {"image_hashes": [], "image_grid_thw": [], "image_embeds": [], "pixel_values": [], "recompute": []}
         has_mm = False
         for seq in seqs:
             n = len(seq)
@@ -170,10 +174,17 @@ class ModelRunner:
                 has_mm = True
                 grids = seq.mm_inputs.get("image_grid_thw")
                 embeds = seq.mm_inputs.get("image_embeds")
+                pixels = seq.mm_inputs.get("pixel_values")
+                p0 = 0
                 for i in range(0 if grids is None else grids.shape[0]):
+                    g = tuple(int(x) for x in grids[i])
                     mm["image_hashes"].append(seq.image_hashes[i])
-                    mm["image_grid_thw"].append(tuple(int(x) for x in grids[i]))
+                    mm["image_grid_thw"].append(g)
                     mm["image_embeds"].append(None if embeds is None else embeds[i])
+                    # pixel_values holds every image's patches back to back (t*h*w rows each)
+                    npatch = g[0] * g[1] * g[2]
+                    mm["pixel_values"].append(None if pixels is None else pixels[p0:p0 + npatch])
+                    p0 += npatch
                     r = seq.images[i].recompute if i < len(seq.images) else None
                     mm["recompute"].append(r if r is not None else 0)
             if seq.is_partial_recompute:
@@ -285,49 +296,75 @@ class ModelRunner:
         return _h2d(np.array([s.temperature for s in seqs], dtype=np.float32), torch.float32, self.device)
 
     # ------------------------------------------------------------------ vision inputs
-    def _image_embeds(self, h: int, grid, given, rows: int | None):
-        """The first `rows` (all when None) visual embeddings of one image.
-
-        An encoder-cache hit reads them back (engine/model_runner.py:366-372); on a
-        miss the caller's `image_embeds` are used, or seeded synthetic embeddings
-        when Config.synthetic_vision opts in, and are stored in the cache.  The
-        vision tower is not part of this path: a miss with neither raises.
-        """
-        hit = self.encoder_cache.get(h, rows)
-        if hit is not None:
-            return hit
+    def _num_units(self, grid) -> int:
         m = self.config.hf_config.spatial_merge_size
-        n = int(grid[0]) * (int(grid[1]) // m) * (int(grid[2]) // m)
-        if given is not None:
-            emb = given.to(self.device, self.dtype)
-        elif self.config.synthetic_vision:
-            g = torch.Generator(device=self.device)
-            g.manual_seed(h & ((1 << 63) - 1))
-            emb = torch.randn(n, self.config.hf_config.hidden_size, generator=g, device=self.device,
-                              dtype=self.dtype)
-        else:
-            raise RuntimeError(
-                f"image {h:#x} is not in the encoder cache and the request carries no image_embeds: the "
-                "vision tower is not part of this build (pass mm_inputs['image_embeds'], or construct the "
-                "engine with synthetic_vision=True for synthetic embeddings)")
-        if emb.shape[0] != n:
-            raise ValueError(f"image_embeds has {emb.shape[0]} rows, the grid {tuple(grid)} gives {n}")
-        self.encoder_cache.put(h, emb)
-        return emb if rows is None else emb[:rows]
+        return int(grid[0]) * (int(grid[1]) // m) * (int(grid[2]) // m)
 
     def _process_visual(self, mm: dict):
-        parts = []
-        for h, grid, given, r in zip(mm["image_hashes"], mm["image_grid_thw"], mm["image_embeds"], mm["recompute"]):
-            # a reused image needs only its first R embeddings (engine/model_runner.py:398-403)
-            parts.append(self._image_embeds(h, grid, given, r if r > 0 else None))
-        return torch.cat(parts, dim=0) if parts else None
+        """Visual embeddings of every image of the batch, cache first (engine/model_runner.py:347-405).
+
+        A hit reads the image's first R rows back (all rows when R is 0).  Misses
+        take the caller's image_embeds when given; those with pixel_values run
+        through the vision tower in one call (the time of that call is vit_time),
+        an image repeated in the batch once; every new result is offered to the
+        cache.  A miss with neither uses seeded synthetic embeddings when
+        Config.synthetic_vision opts in and raises otherwise.
+        """
+        hashes, grids = mm["image_hashes"], mm["image_grid_thw"]
+        out: list = [None] * len(hashes)
+        run: dict[int, list[int]] = {}          # hash -> indices waiting for the vision tower
+        vit_time = 0.0
+        for i, (h, grid, given, pix, r) in enumerate(zip(hashes, grids, mm["image_embeds"], mm["pixel_values"],
+                                                         mm["recompute"])):
+            rows = r if r > 0 else None
+            hit = self.encoder_cache.get(h, rows)
+            if hit is not None:
+                out[i] = hit
+                continue
+            n = self._num_units(grid)
+            if given is not None:
+                emb = given.to(self.device, self.dtype)
+            elif h in run:
+                run[h].append(i)
+                continue
+            elif pix is not None and self.model.visual is not None:
+                run[h] = [i]
+                continue
+            elif self.config.synthetic_vision:
+                g = torch.Generator(device=self.device)
+                g.manual_seed(h & ((1 << 63) - 1))
+                emb = torch.randn(n, self.config.hf_config.hidden_size, generator=g, device=self.device,
+                                  dtype=self.dtype)
+            else:
+                why = ("the request carries no pixel_values or image_embeds" if self.model.visual is not None
+                       else "the model has no vision tower (pass mm_inputs['image_embeds'], or construct the "
+                            "engine with synthetic_vision=True for synthetic embeddings)")
+                raise RuntimeError(f"image {h:#x} is not in the encoder cache and {why}")
+            if emb.shape[0] != n:
+                raise ValueError(f"image_embeds has {emb.shape[0]} rows, the grid {tuple(grid)} gives {n}")
+            self.encoder_cache.put(h, emb)
+            out[i] = emb if rows is None else emb[:rows]
+        if run:
+            first = [idx[0] for idx in run.values()]
+            pv = torch.cat([mm["pixel_values"][i].to(self.device) for i in first], dim=0)
+            torch.cuda.synchronize(self.device)
+            t0 = perf_counter()
+            emb_all = self.model.get_visual_features(pv, [grids[i] for i in first])
+            torch.cuda.synchronize(self.device)
+            vit_time = perf_counter() - t0
+            for (h, idx), emb in zip(run.items(), torch.split(emb_all, [self._num_units(grids[i]) for i in first])):
+                self.encoder_cache.put(h, emb)
+                for i in idx:
+                    r = mm["recompute"][i]
+                    out[i] = emb if r <= 0 else emb[:r]
+        return (torch.cat(out, dim=0) if out else None), vit_time
 
     # ------------------------------------------------------------------ execution
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_prefill, mm=None):
-        visual = self._process_visual(mm) if (is_prefill and mm) else None
+        visual, vit_time = self._process_visual(mm) if (is_prefill and mm) else (None, 0.0)
         hidden = self.model(input_ids, positions, visual)
-        return self.model.compute_logits(hidden), 0.0
+        return self.model.compute_logits(hidden), vit_time
 
     @torch.inference_mode()
     def run(self, seqs: list[Sequence], is_prefill: bool):

@@ -499,3 +499,38 @@ def decode_attention_noalloc(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
         _stream(q))
     _lib.check("vlc_decode_attn_noalloc", st)
     return out
+
+
+# --------------------------------------------------------------------------- vision tower
+def vision_rope_pad(qkv: torch.Tensor, pos_hw: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                    num_heads: int, head_dim: int, padded_dim: int = HEAD_DIM,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """2-D rotary of the vision tower's q and k, split into padded head rows (vlc_vision_rope_pad).
+
+    qkv: [N, 3 * num_heads * head_dim] bf16 (rows 16-byte aligned); pos_hw: int32
+    [N, 2] (patch row, patch column); cos/sin tables: bf16 [max_pos, head_dim // 4].
+    Returns out [N, 3, num_heads, padded_dim] bf16: q, k rotated, v copied, dims
+    head_dim.. zero.
+    """
+    _require_device("vision_rope_pad", qkv, pos_hw, cos_table, sin_table, out)
+    n = qkv.shape[0]
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.shape[1] != 3 * num_heads * head_dim or qkv.stride(1) != 1:
+        raise ValueError(f"qkv must be bf16 [N, {3 * num_heads * head_dim}] with contiguous rows")
+    if pos_hw.dtype != torch.int32 or tuple(pos_hw.shape) != (n, 2) or not pos_hw.is_contiguous():
+        raise ValueError("pos_hw must be contiguous int32 [N, 2]")
+    q4 = head_dim // 4
+    for name, t in (("cos_table", cos_table), ("sin_table", sin_table)):
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.shape[1] != q4 or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous bf16 [max_pos, {q4}]")
+    if cos_table.shape != sin_table.shape:
+        raise ValueError("cos_table and sin_table differ in shape")
+    if out is None:
+        out = torch.empty(n, 3, num_heads, padded_dim, dtype=torch.bfloat16, device=qkv.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (n, 3, num_heads, padded_dim) or \
+            out.stride(3) != 1 or out.stride(2) != padded_dim or out.stride(1) != num_heads * padded_dim:
+        raise ValueError(f"out must be bf16 [N, 3, {num_heads}, {padded_dim}] with contiguous token rows")
+    st = _lib.load().vlc_vision_rope_pad(
+        qkv.data_ptr(), qkv.stride(0), pos_hw.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+        cos_table.shape[0], n, num_heads, head_dim, padded_dim, out.data_ptr(), out.stride(0), _stream(qkv))
+    _lib.check("vlc_vision_rope_pad", st)
+    return out

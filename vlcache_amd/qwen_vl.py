@@ -9,40 +9,25 @@ image-token rows of the embeddings are replaced by visual embeddings).
 GEMMs, norms and the MLP stay on torch (hipBLASLt) and run eagerly; per layer
 the rotary embedding of q and k and the KV store run as one gfx950 kernel and
 the attention as another, via layers.attention.Attention.
-The vision tower is not part of this path: visual embeddings come from the
-encoder cache (warm request) or are supplied by the caller.
+When the model config carries a vision_config the model owns the vision tower
+(vision.VisionTransformer, the cold path behind the encoder cache).
 Weights are random N(0, 0.02) unless loaded by the caller.
 """
 from __future__ import annotations
+
+import re
 
 import torch
 import torch.nn.functional as F
 from torch import nn
 
 from .layers.attention import Attention
+from .layers.layernorm import RMSNorm
+from .vision import VisionTransformer, vision_config
 from .layers.rotary_embedding import get_rope
 from .utils.context import get_context
 
 IMAGE_TOKEN_ID = 151655
-
-
-class RMSNorm(nn.Module):
-    """(add +) RMSNorm with fp32 statistics (layers/layernorm.py:16-40)."""
-
-    def __init__(self, hidden_size: int, eps: float = 1e-6):
-        super().__init__()
-        self.eps = eps
-        self.weight = nn.Parameter(torch.ones(hidden_size))
-
-    def forward(self, x, residual=None):
-        dtype = x.dtype
-        xf = x.float()
-        if residual is not None:
-            xf = xf + residual.float()
-            residual = xf.to(dtype)
-        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        out = xf.to(dtype) * self.weight
-        return out if residual is None else (out, residual)
 
 
 class DecoderAttention(nn.Module):
@@ -130,10 +115,18 @@ class Qwen2_5_VLForConditionalGeneration(nn.Module):
     def __init__(self, cfg):
         super().__init__()
         self.config = cfg
+        vcfg = getattr(cfg, "vision_config", None)
+        self.visual = (VisionTransformer(vision_config(vcfg, cfg.hidden_size), eps=cfg.rms_norm_eps)
+                       if vcfg is not None else None)
         self.model = TextModel(cfg)
         self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
         if getattr(cfg, "tie_word_embeddings", False):
             self.lm_head.weight = self.model.embed_tokens.weight
+
+    def get_visual_features(self, pixel_values, grid_thw):
+        if self.visual is None:
+            raise RuntimeError("the model config has no vision_config: there is no vision tower")
+        return self.visual(pixel_values, grid_thw)
 
     def forward(self, input_ids, positions, visual_embeds=None):
         inputs_embeds = self.model.embed_tokens(input_ids)
@@ -157,7 +150,7 @@ def random_init_(model: nn.Module, std: float = 0.02, seed: int = 0) -> None:
     g = torch.Generator(device=next(model.parameters()).device)
     g.manual_seed(seed)
     for name, p in model.named_parameters():
-        if name.endswith("layernorm.weight") or name.endswith("norm.weight"):
+        if re.search(r"(norm\d?|ln_q)\.weight$", name):
             p.fill_(1.0)
         elif name.endswith(".bias"):
             p.zero_()
