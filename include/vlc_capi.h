@@ -289,6 +289,38 @@ int vlc_vision_rope_pad(const void* qkv, int64_t qkv_row_stride, const int32_t* 
                         int64_t num_tokens, int num_heads, int head_dim, int padded_dim,
                         void* out, int64_t out_row_stride, void* stream);
 
+/*
+ * RMSNorm, optionally with the residual add fused in front of it.
+ * Replaces RMSNorm.rms_forward / add_rms_forward (layers/layernorm.py:16-40),
+ * used by the decoder (models/qwen3.py:145-158, :184) and the vision tower
+ * (models/qwen2_5_vl.py:292-305, :330).
+ *
+ * x, residual, residual_out, out: [num_rows, dim] bf16 at their row strides
+ * (elements); weight: bf16 [dim].
+ *   residual == NULL: out = bf16(bf16(x * r) * weight), r = rsqrt(mean(x^2) + eps);
+ *   otherwise:        s = x + residual in fp32, residual_out = bf16(s),
+ *                     out = bf16(bf16(s * r) * weight) with r from the fp32 s.
+ * residual_out may be residual or x (each element is read before it is written);
+ * out must not overlap residual_out.  dim % 8 == 0, dim <= 8192; pointers 16-byte
+ * aligned and row strides multiples of 8 elements.
+ */
+int vlc_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                 void* residual_out, int64_t residual_out_row_stride, const void* weight, float eps,
+                 int64_t num_rows, int64_t dim, void* out, int64_t out_row_stride, void* stream);
+
+/*
+ * SiLU-and-multiply of a packed [gate | up] projection.
+ * Replaces SiluAndMul (layers/activation.py:8-14), used by the decoder MLP
+ * (models/qwen3.py:97-110) and the vision MLP (models/qwen2_5_vl.py:219-243).
+ *
+ * gate_up: [num_rows, 2 * inter] bf16 at gate_up_row_stride (gate columns
+ * [0, inter), up columns [inter, 2 * inter)); out[n][i] = bf16(silu(gate) * up)
+ * with fp32 math, silu(g) = g / (1 + exp(-g)).  inter % 4 == 0; pointers 8-byte
+ * aligned and row strides multiples of 4 elements.
+ */
+int vlc_silu_mul(const void* gate_up, int64_t gate_up_row_stride, int64_t num_rows, int64_t inter,
+                 void* out, int64_t out_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,91 @@
+"""GPU parity of vlc_rms_norm and vlc_silu_mul against the CPU oracle (oracle/layers.py).
+
+The new residual (a bf16 rounding of an fp32 sum of two bf16 values) is bit-exact.
+The normalised output may differ from the oracle's in rare elements: the row's
+sum of squares is accumulated in another order, so rsqrt can move by an fp32 ulp,
+a normalised value at a bf16 rounding boundary can round the other way (one bf16
+ulp), and the weight multiply rounds that difference again (up to two ulps of the
+output).  SiLU-and-multiply rounds once (the device exp differs from the host's
+in the last fp32 bits: at most one ulp).  Bars: |out - ref| <= 2^-6 |ref| for
+RMSNorm, 2^-7 |ref| for SiLU-and-multiply, and the fraction of bit-exact
+elements is printed.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import layers as ol
+from tests._util import randn_bf16, say
+from vlcache_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def _within_ulps(got, ref, what, ulps=1):
+    g, r = got.float().cpu(), ref.float().cpu()
+    bad = (g - r).abs() > r.abs() * (ulps * 2.0 ** -7)
+    n = int(bad.sum())
+    exact = float((g == r).float().mean())
+    print(f"{what}: {exact:.6f} of elements bit-exact", flush=True)
+    assert n == 0, f"{what}: {n} elements beyond {ulps} bf16 ulp(s)"
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 64), (7, 1280), (1247, 2048), (42196, 1280), (33, 3584), (5, 8192),
+                                      (129, 5120)])
+@pytest.mark.parametrize("with_residual", [False, True], ids=["plain", "residual"])
+def test_rms_norm(dev, rows, dim, with_residual):
+    say(f"rms_norm rows={rows} dim={dim} residual={with_residual}")
+    x = randn_bf16((rows, dim), rows + dim, 2.0)
+    w = (randn_bf16((dim,), 3) * 0.2 + 1).to(torch.bfloat16)
+    xd, wd = x.to(dev), w.to(dev)
+    if with_residual:
+        r = randn_bf16((rows, dim), 7)
+        out, new_res = kernels.rms_norm(xd, wd, 1e-6, r.to(dev), residual_out=torch.empty_like(xd))
+        ref, ref_res = ol.rms_norm(x, w, 1e-6, r)
+        assert torch.equal(new_res.cpu().view(torch.int16), ref_res.view(torch.int16))
+    else:
+        out = kernels.rms_norm(xd, wd, 1e-6)
+        ref = ol.rms_norm(x, w, 1e-6)
+    _within_ulps(out, ref, f"rms_norm {rows}x{dim}", 2)
+
+
+def test_rms_norm_strided_rows_and_in_place_residual(dev):
+    """x a strided view (row stride 3 * dim); the new residual written over the old one."""
+    say("rms_norm: strided x, residual updated in place")
+    rows, dim = 300, 2048
+    big = randn_bf16((rows, 3 * dim), 11)
+    x = big[:, dim:2 * dim]
+    r = randn_bf16((rows, dim), 12)
+    w = randn_bf16((dim,), 13)
+    rd = r.to(dev)
+    out, new_res = kernels.rms_norm(big.to(dev)[:, dim:2 * dim], w.to(dev), 1e-6, rd)
+    assert new_res.data_ptr() == rd.data_ptr()
+    ref, ref_res = ol.rms_norm(x, w, 1e-6, r)
+    assert torch.equal(rd.cpu().view(torch.int16), ref_res.view(torch.int16))
+    _within_ulps(out, ref, "rms_norm strided", 2)
+
+
+def test_rms_norm_rejects_bad_shapes(dev):
+    x = torch.zeros(4, 100, dtype=torch.bfloat16, device=dev)       # dim % 8 != 0
+    with pytest.raises(Exception):
+        kernels.rms_norm(x, torch.ones(100, dtype=torch.bfloat16, device=dev), 1e-6)
+    x = torch.zeros(4, 64, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        kernels.rms_norm(x, torch.ones(64, dtype=torch.float32, device=dev), 1e-6)
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 4), (1247, 11008), (4219, 3420), (3, 18944)])
+def test_silu_mul(dev, rows, inter):
+    say(f"silu_mul rows={rows} inter={inter}")
+    gu = randn_bf16((rows, 2 * inter), rows + inter, 3.0)
+    out = kernels.silu_mul(gu.to(dev))
+    _within_ulps(out, ol.silu_mul(gu), f"silu_mul {rows}x{inter}")
+
+
+def test_silu_mul_extremes(dev):
+    """Large |gate|: silu(-100) * up = -0 (exp overflows to inf), silu(100) = 100; 0 -> 0."""
+    g = torch.tensor([[-100.0, 100.0, 0.0, -1e30]]).to(torch.bfloat16)
+    u = torch.tensor([[3.0, 2.0, 5.0, 1.0]]).to(torch.bfloat16)
+    out = kernels.silu_mul(torch.cat([g, u], 1).to(dev)).float().cpu()
+    assert out.tolist() == [[-0.0, 200.0, 0.0, -0.0]]

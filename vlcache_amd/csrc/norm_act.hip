@@ -1,0 +1,185 @@
+// RMSNorm (with the fused residual add) and SiLU-and-multiply for the decoder
+// and the vision tower: one launch each instead of torch's chain of eager
+// elementwise and reduction kernels.
+//
+// rms_norm follows layers/layernorm.py:16-40 of the reference:
+//   without residual: y = bf16( bf16(x * r) * w ),             r = rsqrt(mean(x^2) + eps)
+//   with residual:    s = x + res (fp32); res_out = bf16(s);  y = bf16( bf16(s * r) * w ),
+//                     r from the fp32 s (not the rounded res_out);
+// statistics in fp32.  A wave owns a row: each lane holds its 16-byte chunks
+// in registers between the sum of squares and the scaling, so a row is read
+// once and written once.  The sum runs lane-serially over the lane's chunks,
+// then across the wave by butterfly.
+//
+// silu_mul follows layers/activation.py:8-14 (SiluAndMul: chunk the last dim
+// into gate and up, silu(gate) * up) with fp32 math and one rounding to bf16,
+// as the reference's compiled kernel computes it.  A lane owns 4 elements.
+#include "common.h"
+
+namespace vlc {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / 64;
+
+__device__ __forceinline__ float lo16(uint32_t w) { return bf16_bits_to_f32(w & 0xffffu); }
+__device__ __forceinline__ float hi16(uint32_t w) { return bf16_bits_to_f32(w >> 16); }
+__device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// CPL = chunks (of 8 elements) per lane, rounded up: dim <= 64 * CPL * 8.
+template <int CPL, bool kResidual>
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(
+    const char* x, int64_t x_stride_b, const char* res, int64_t res_stride_b, char* res_out,
+    int64_t res_out_stride_b, const char* __restrict__ weight, float eps, int64_t rows, int chunks,
+    float inv_dim, char* out, int64_t out_stride_b) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float s[CPL][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(x + row * x_stride_b + c * 16);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+      if constexpr (kResidual) {
+        const u32x4 b = *reinterpret_cast<const u32x4*>(res + row * res_stride_b + c * 16);
+        const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+        uint32_t ro[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          s[i][2 * k] = lo16(aw[k]) + lo16(bw[k]);
+          s[i][2 * k + 1] = hi16(aw[k]) + hi16(bw[k]);
+          ro[k] = pack2(s[i][2 * k], s[i][2 * k + 1]);
+        }
+        *reinterpret_cast<u32x4*>(res_out + row * res_out_stride_b + c * 16) = u32x4{ro[0], ro[1], ro[2], ro[3]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          s[i][2 * k] = lo16(aw[k]);
+          s[i][2 * k + 1] = hi16(aw[k]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += s[i][e] * s[i][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss * inv_dim + eps);
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) {
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(weight + c * 16);
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        o[k] = pack2(rbf(s[i][2 * k] * r) * lo16(ww[k]), rbf(s[i][2 * k + 1] * r) * hi16(ww[k]));
+      *reinterpret_cast<u32x4*>(out + row * out_stride_b + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
+template <int CPL>
+int launch_rms(const void* x, int64_t xs, const void* res, int64_t rs, void* ro, int64_t ros, const void* w,
+               float eps, int64_t rows, int dim, void* out, int64_t os, hipStream_t st) {
+  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const float inv_dim = 1.0f / (float)dim;
+  if (res)
+    hipLaunchKernelGGL((rms_norm_kernel<CPL, true>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
+                       static_cast<const char*>(x), xs * 2, static_cast<const char*>(res), rs * 2,
+                       static_cast<char*>(ro), ros * 2, static_cast<const char*>(w), eps, rows, dim / 8, inv_dim,
+                       static_cast<char*>(out), os * 2);
+  else
+    hipLaunchKernelGGL((rms_norm_kernel<CPL, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
+                       static_cast<const char*>(x), xs * 2, nullptr, 0, nullptr, 0, static_cast<const char*>(w),
+                       eps, rows, dim / 8, inv_dim, static_cast<char*>(out), os * 2);
+  return launch_status();
+}
+
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const char* __restrict__ gu, int64_t gu_stride_b,
+                                                            int64_t rows, int quads, int64_t up_offset_b,
+                                                            char* __restrict__ out, int64_t out_stride_b) {
+  const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (u >= rows * quads) return;
+  const int64_t row = u / quads;
+  const int q = (int)(u - row * quads);
+  const char* src = gu + row * gu_stride_b + (int64_t)q * 8;
+  const uint2 g = *reinterpret_cast<const uint2*>(src);
+  const uint2 p = *reinterpret_cast<const uint2*>(src + up_offset_b);
+  const float gv[4] = {lo16(g.x), hi16(g.x), lo16(g.y), hi16(g.y)};
+  const float pv[4] = {lo16(p.x), hi16(p.x), lo16(p.y), hi16(p.y)};
+  float y[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) y[k] = gv[k] / (1.0f + expf(-gv[k])) * pv[k];
+  *reinterpret_cast<uint2*>(out + row * out_stride_b + (int64_t)q * 8) = uint2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+}
+
+}  // namespace
+}  // namespace vlc
+
+VLC_API int vlc_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                         void* residual_out, int64_t residual_out_row_stride, const void* weight, float eps,
+                         int64_t num_rows, int64_t dim, void* out, int64_t out_row_stride, void* stream) {
+  using namespace vlc;
+  if (num_rows < 0 || dim <= 0 || dim % 8 != 0 || dim > 64 * 16 * 8 || !(eps >= 0.f)) return VLC_ERR_INVALID;
+  if (x_row_stride < dim || out_row_stride < dim) return VLC_ERR_INVALID;
+  if (residual && (residual_row_stride < dim || !residual_out || residual_out_row_stride < dim))
+    return VLC_ERR_INVALID;
+  if (num_rows == 0) return VLC_OK;
+  if (!x || !weight || !out) return VLC_ERR_INVALID;
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) || (x_row_stride % 8) || (out_row_stride % 8))
+    return VLC_ERR_UNSUPPORTED;
+  if (residual && (!aligned16(residual) || !aligned16(residual_out) || (residual_row_stride % 8) ||
+                   (residual_out_row_stride % 8)))
+    return VLC_ERR_UNSUPPORTED;
+  const int chunks = (int)(dim / 8);
+  const int cpl = (chunks + 63) / 64;
+  hipStream_t s = as_stream(stream);
+#define VLC_RMS_CASE(N) \
+  case N:               \
+    return launch_rms<N>(x, x_row_stride, residual, residual_row_stride, residual_out, residual_out_row_stride, \
+                         weight, eps, num_rows, (int)dim, out, out_row_stride, s);
+  switch (cpl) {
+    VLC_RMS_CASE(1) VLC_RMS_CASE(2) VLC_RMS_CASE(3) VLC_RMS_CASE(4) VLC_RMS_CASE(5) VLC_RMS_CASE(6)
+    VLC_RMS_CASE(7) VLC_RMS_CASE(8)
+    case 9: case 10: case 11: case 12:
+      return launch_rms<12>(x, x_row_stride, residual, residual_row_stride, residual_out, residual_out_row_stride,
+                            weight, eps, num_rows, (int)dim, out, out_row_stride, s);
+    default:
+      return launch_rms<16>(x, x_row_stride, residual, residual_row_stride, residual_out, residual_out_row_stride,
+                            weight, eps, num_rows, (int)dim, out, out_row_stride, s);
+  }
+#undef VLC_RMS_CASE
+}
+
+VLC_API int vlc_silu_mul(const void* gate_up, int64_t gate_up_row_stride, int64_t num_rows, int64_t inter,
+                         void* out, int64_t out_row_stride, void* stream) {
+  using namespace vlc;
+  if (num_rows < 0 || inter <= 0 || inter % 4 != 0) return VLC_ERR_INVALID;
+  if (gate_up_row_stride < 2 * inter || out_row_stride < inter) return VLC_ERR_INVALID;
+  if (num_rows == 0) return VLC_OK;
+  if (!gate_up || !out) return VLC_ERR_INVALID;
+  if ((reinterpret_cast<uintptr_t>(gate_up) & 7) || (reinterpret_cast<uintptr_t>(out) & 7) ||
+      (gate_up_row_stride % 4) || (out_row_stride % 4))
+    return VLC_ERR_UNSUPPORTED;
+  const int quads = (int)(inter / 4);
+  const int64_t total = num_rows * quads;
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  if (blocks >= ((int64_t)1 << 31)) return VLC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream),
+                     static_cast<const char*>(gate_up), gate_up_row_stride * 2, num_rows, quads, inter * 2,
+                     static_cast<char*>(out), out_row_stride * 2);
+  return launch_status();
+}

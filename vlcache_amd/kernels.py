@@ -534,3 +534,68 @@ def vision_rope_pad(qkv: torch.Tensor, pos_hw: torch.Tensor, cos_table: torch.Te
         cos_table.shape[0], n, num_heads, head_dim, padded_dim, out.data_ptr(), out.stride(0), _stream(qkv))
     _lib.check("vlc_vision_rope_pad", st)
     return out
+
+
+# --------------------------------------------------------------------------- norm and activation
+def _rows2d(name: str, t: torch.Tensor, dim: int) -> None:
+    if t.dtype != torch.bfloat16 or t.dim() != 2 or t.shape[1] != dim or t.stride(1) != 1:
+        raise ValueError(f"{name} must be bf16 [rows, {dim}] with contiguous rows, got "
+                         f"{tuple(t.shape)} {t.dtype}")
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+             out: torch.Tensor | None = None, residual_out: torch.Tensor | None = None):
+    """RMSNorm of x [rows, dim] bf16 (vlc_rms_norm); with residual, of x + residual.
+
+    Returns out, or (out, residual_out) when residual is given: residual_out =
+    bf16(x + residual) (written in place into `residual` when residual_out is
+    None), out the normalised fp32 sum times weight.
+    """
+    _require_device("rms_norm", x, weight, residual, out, residual_out)
+    lead = x.shape[:-1]
+    dim = x.shape[-1]
+    x2 = x.reshape(-1, dim)
+    _rows2d("x", x2, dim)
+    if weight.dtype != torch.bfloat16 or weight.shape != (dim,) or not weight.is_contiguous():
+        raise ValueError(f"weight must be contiguous bf16 [{dim}]")
+    rows = x2.shape[0]
+    o = torch.empty(rows, dim, dtype=torch.bfloat16, device=x.device) if out is None else out.reshape(-1, dim)
+    _rows2d("out", o, dim)
+    if residual is not None:
+        r2 = residual.reshape(-1, dim)
+        _rows2d("residual", r2, dim)
+        ro = r2 if residual_out is None else residual_out.reshape(-1, dim)
+        _rows2d("residual_out", ro, dim)
+        if r2.shape[0] != rows or ro.shape[0] != rows:
+            raise ValueError("x and residual differ in rows")
+        rp, rs, rop, ros = r2.data_ptr(), r2.stride(0), ro.data_ptr(), ro.stride(0)
+    else:
+        rp, rs, rop, ros = None, 0, None, 0
+    if o.shape[0] != rows:
+        raise ValueError("out has the wrong number of rows")
+    st = _lib.load().vlc_rms_norm(x2.data_ptr(), x2.stride(0), rp, rs, rop, ros, weight.data_ptr(), float(eps),
+                                  rows, dim, o.data_ptr(), o.stride(0), _stream(x))
+    _lib.check("vlc_rms_norm", st)
+    o = o.view(*lead, dim)
+    if residual is None:
+        return o
+    return o, ro.view(*lead, dim)
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up of a packed [rows, 2 * inter] bf16 projection (vlc_silu_mul) -> [rows, inter]."""
+    _require_device("silu_mul", gate_up, out)
+    lead = gate_up.shape[:-1]
+    two = gate_up.shape[-1]
+    if two % 2:
+        raise ValueError("gate_up's last dim must be even")
+    inter = two // 2
+    g2 = gate_up.reshape(-1, two)
+    _rows2d("gate_up", g2, two)
+    rows = g2.shape[0]
+    o = torch.empty(rows, inter, dtype=torch.bfloat16, device=gate_up.device) if out is None else out.reshape(-1, inter)
+    _rows2d("out", o, inter)
+    st = _lib.load().vlc_silu_mul(g2.data_ptr(), g2.stride(0), rows, inter, o.data_ptr(), o.stride(0),
+                                  _stream(gate_up))
+    _lib.check("vlc_silu_mul", st)
+    return o.view(*lead, inter)

@@ -1,8 +1,16 @@
-"""RMSNorm with an optional fused residual add (layers/layernorm.py:5-50 of the reference)."""
+"""RMSNorm with an optional fused residual add (layers/layernorm.py:5-50 of the reference).
+
+One gfx950 kernel per call (vlc_rms_norm): fp32 statistics, the residual sum
+rounded to bf16 for the next layer while the norm uses the fp32 sum, the
+normalised value rounded to bf16 before the weight multiply, as the
+reference's rms_forward / add_rms_forward compute.
+"""
 from __future__ import annotations
 
 import torch
 from torch import nn
+
+from .. import kernels
 
 
 class RMSNorm(nn.Module):
@@ -14,11 +22,7 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(hidden_size))
 
     def forward(self, x, residual=None):
-        dtype = x.dtype
-        xf = x.float()
-        if residual is not None:
-            xf = xf + residual.float()
-            residual = xf.to(dtype)
-        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        out = xf.to(dtype) * self.weight
-        return out if residual is None else (out, residual)
+        if residual is None:
+            return kernels.rms_norm(x, self.weight, self.eps)
+        # the new residual goes to a fresh tensor: callers may still hold the old one
+        return kernels.rms_norm(x, self.weight, self.eps, residual, residual_out=torch.empty_like(residual))

@@ -6,9 +6,10 @@ Qwen2.5-VL variant: QKV bias, no q/k norm) and of
 Qwen2_5_VLForConditionalGeneration.forward (models/qwen2_5_vl.py:562-580: the
 image-token rows of the embeddings are replaced by visual embeddings).
 
-GEMMs, norms and the MLP stay on torch (hipBLASLt) and run eagerly; per layer
-the rotary embedding of q and k and the KV store run as one gfx950 kernel and
-the attention as another, via layers.attention.Attention.
+GEMMs stay on torch (hipBLASLt) and run eagerly; per layer the rotary
+embedding of q and k and the KV store run as one gfx950 kernel and the
+attention as another (layers.attention.Attention), each RMSNorm (with its
+residual add) as one kernel and the MLP's SiLU-and-multiply as one.
 When the model config carries a vision_config the model owns the vision tower
 (vision.VisionTransformer, the cold path behind the encoder cache).
 Weights are random N(0, 0.02) unless loaded by the caller.
@@ -18,14 +19,14 @@ from __future__ import annotations
 import re
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
+from . import kernels
 from .layers.attention import Attention
 from .layers.layernorm import RMSNorm
-from .vision import VisionTransformer, vision_config
 from .layers.rotary_embedding import get_rope
 from .utils.context import get_context
+from .vision import VisionTransformer, vision_config
 
 IMAGE_TOKEN_ID = 151655
 
@@ -71,8 +72,7 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x):
-        gu = self.gate_up_proj(x)
-        return self.down_proj(F.silu(gu[..., :self.inter]) * gu[..., self.inter:])
+        return self.down_proj(kernels.silu_mul(self.gate_up_proj(x)))
 
 
 class DecoderLayer(nn.Module):

@@ -17,7 +17,8 @@ On gfx950:
     causal=False and cu_seqlens_q == cu_seqlens_k, :200-210); the 80-dim heads
     are zero-padded to the kernel's 128 dims, which leaves q.k and the first 80
     output dims unchanged; one work plan per boundary list serves every block;
-  * GEMMs, norms and activations run on torch (hipBLASLt).
+  * each RMSNorm (with its residual add) and the MLP's SiLU-and-multiply run
+    as one kernel each; GEMMs and the merger's GELU run on torch (hipBLASLt).
 
 As in the reference, the rotary angles are rounded to bf16 before cos/sin
 (:486-487) and the rotation itself is bf16 arithmetic.  The Conv3d patch
@@ -30,7 +31,6 @@ from types import SimpleNamespace
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from . import kernels
@@ -105,7 +105,7 @@ class VisionLayout:
 
 
 class VisionMLP(nn.Module):
-    """SwiGLU with biases (models/qwen2_5_vl.py:219-243)."""
+    """SwiGLU with biases (models/qwen2_5_vl.py:219-243); SiLU-and-multiply as one kernel."""
 
     def __init__(self, dim: int, inter: int):
         super().__init__()
@@ -114,8 +114,7 @@ class VisionMLP(nn.Module):
         self.down_proj = nn.Linear(inter, dim, bias=True)
 
     def forward(self, x):
-        gu = self.gate_up_proj(x)
-        return self.down_proj(F.silu(gu[..., :self.inter]) * gu[..., self.inter:])
+        return self.down_proj(kernels.silu_mul(self.gate_up_proj(x)))
 
 
 class VisionAttention(nn.Module):
