@@ -281,8 +281,8 @@ int vlc_decode_attn_noalloc(const void* q, int64_t q_row_stride, const void* k_c
  *   reference's bf16 tensor arithmetic rounds; v is copied.
  * out: [num_tokens][3][num_heads][padded_dim] bf16 at row stride out_row_stride;
  *   dims head_dim..padded_dim-1 of every head are written as zero.
- * head_dim % 16 == 0, padded_dim % 8 == 0, padded_dim >= head_dim; qkv, out and
- * their row strides 16-byte aligned.
+ * head_dim % 16 == 0, padded_dim % 8 == 0, head_dim <= padded_dim <= 128; qkv,
+ * out and their row strides 16-byte aligned, the tables 8-byte aligned.
  */
 int vlc_vision_rope_pad(const void* qkv, int64_t qkv_row_stride, const int32_t* pos_hw,
                         const void* cos_table, const void* sin_table, int64_t max_pos,
