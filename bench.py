@@ -24,7 +24,8 @@ holding clean lines of other data; median), next to a plain device copy of the
 same bytes timed the same way; both are also reported after a 512 MiB write,
 which leaves the MALL full of dirty lines whose write-backs compete.
 The paged decode attention of the batched 7B tail (batch 4, ~13.4k context) is
-timed cold on its own (kernels.decode).
+timed cold on its own (kernels.decode); the vision tower on one 4K image (the
+cold path that fills the encoder cache) is timed whole and per attention kernel.
 """
 from __future__ import annotations
 
@@ -468,6 +469,88 @@ def run_decode(reps: int = 10):
     }
 
 
+def run_vision(reps: int = 5):
+    """The vision tower on one 4K image (grid (1, 154, 274): 42196 patches -> 10549 tokens).
+
+    Random-init public configuration (32 blocks of hidden 1280, 16 heads of 80 dims,
+    whole-image attention at blocks 7/15/23/31, window 112 px).  Whole forward:
+    HIP events around each of `reps` calls after one warm-up, median.  The three
+    kernels of a block's attention on the same layout, each the median of 20
+    event-timed calls: the fused rotary + head padding (HBM: bytes read + written),
+    the window attention and the whole-image attention (MFMA: 4 * pairs * 80 dims
+    * 16 heads useful flops; the kernel runs 128-dim padded heads).
+    """
+    from vlcache_amd import kernels
+    from vlcache_amd.config import QWEN25_VL_VISION
+    from vlcache_amd.qwen_vl import random_init_
+    from vlcache_amd.vision import VisionTransformer, vision_config
+
+    dev = torch.device("cuda:0")
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            vt = VisionTransformer(vision_config(dict(QWEN25_VL_VISION), 2048))
+    finally:
+        torch.set_default_dtype(prev)
+    random_init_(vt)
+    vt.eval()
+    grids = [(1, 154, 274)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    pix = torch.randn(154 * 274, 1176, generator=g, device=dev)
+    vt(pix, grids)
+    torch.cuda.synchronize()
+    ev = _events(reps)
+    for a, b in ev:
+        a.record()
+        vt(pix, grids)
+        b.record()
+    torch.cuda.synchronize()
+    fwd = sorted(a.elapsed_time(b) for a, b in ev)[reps // 2]
+    run = vt._prepare(grids)
+    lay = run.layout
+    n, h, hd = lay.num_patches, vt.cfg.num_heads, vt.head_dim
+    qkv = torch.randn(n, 3 * h * hd, generator=g, device=dev, dtype=torch.bfloat16)
+    heads = kernels.vision_rope_pad(qkv, run.pos_hw, run.cos, run.sin, h, hd)
+    o = torch.empty(n, h, kernels.HEAD_DIM, dtype=torch.bfloat16, device=dev)
+
+    def med_ms(fn, k=20):
+        fn()
+        torch.cuda.synchronize()
+        e = _events(k)
+        for a, b in e:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return sorted(a.elapsed_time(b) for a, b in e)[k // 2]
+
+    rope_ms = med_ms(lambda: kernels.vision_rope_pad(qkv, run.pos_hw, run.cos, run.sin, h, hd, out=heads))
+    rope_bytes = n * (3 * h * hd * 2 + 3 * h * kernels.HEAD_DIM * 2)
+
+    def attn(cu, plan):
+        return lambda: kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu, cu, hd ** -0.5,
+                                                causal=False, plan=plan, out=o)
+
+    out = {"workload": "Qwen2.5-VL vision tower (public config, random init), one 4K image: grid (1, 154, 274), "
+                       "42196 patches -> 10549 tokens",
+           "forward_ms": round(fwd, 2), "timing": f"HIP events, median of {reps} forwards after 1 warm-up",
+           "rope_pad": {"ms": round(rope_ms, 4), "bytes": rope_bytes,
+                        "gbps": round(rope_bytes / (rope_ms * 1e-3) / 1e9, 1),
+                        "frac_hbm_peak": round(rope_bytes / (rope_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
+    for name, cu_host, cu, plan in (("window_attention", lay.cu_window, run.cu_window, run.plan_window),
+                                    ("whole_image_attention", lay.cu_full, run.cu_full, run.plan_full)):
+        ms = med_ms(attn(cu, plan))
+        pairs = sum((b - a) ** 2 for a, b in zip(cu_host, cu_host[1:]))
+        tf = 4.0 * pairs * hd * h / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "sequences": len(cu_host) - 1, "work_items": plan.num_items,
+                     "useful_tflops": round(tf, 1), "frac_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+    del vt, heads, o, qkv
+    torch.cuda.empty_cache()
+    return out
+
+
 def _cpu_median(fn, runs: int, budget_s: float):
     times = []
     t_start = time.perf_counter()
@@ -539,6 +622,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ttft", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-vision", action="store_true", help="skip the vision tower sub-result")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads' sub-results")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run one plain device-to-device copy of this many MiB (HBM counter calibration)")
@@ -561,6 +645,7 @@ def main():
 
     r = run_gpu(args.steps, args.warmup, args.workload)
     decode = run_decode() if not args.no_decode else None
+    vision = run_vision() if not args.no_vision else None
     others = {}
     if not args.no_configs:
         for name, kw in (("cfg3", {"scatter": True}), ("cfg4", {}), ("cfg5", {})):
@@ -645,6 +730,7 @@ def main():
         },
         "ms_per_step_graph": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
         "warm_ttft": ttft,
+        "vision": vision,
         "configs": others,
     }
     print(json.dumps(line), flush=True)
