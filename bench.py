@@ -648,7 +648,7 @@ def main():
     vision = run_vision() if not args.no_vision else None
     others = {}
     if not args.no_configs:
-        for name, kw in (("cfg3", {"scatter": True}), ("cfg4", {}), ("cfg5", {})):
+        for name, kw in (("cfg1", {"scatter": True}), ("cfg3", {"scatter": True}), ("cfg4", {}), ("cfg5", {})):
             if name != args.workload:
                 others[name] = run_config(name, args.steps, 1, **kw)
     wl, hp = r["wl"], r["hp"]
