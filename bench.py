@@ -478,7 +478,7 @@ def run_vision(reps: int = 5):
     kernels of a block's attention on the same layout, each the median of 20
     event-timed calls: the fused rotary + head padding (HBM: bytes read + written),
     the window attention and the whole-image attention (MFMA: 4 * pairs * 80 dims
-    * 16 heads useful flops; the kernel runs 128-dim padded heads).
+    * 16 heads; the kernel's 80-dim variant skips the heads' zero padding).
     """
     from vlcache_amd import kernels
     from vlcache_amd.config import QWEN25_VL_VISION
@@ -531,7 +531,7 @@ def run_vision(reps: int = 5):
 
     def attn(cu, plan):
         return lambda: kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu, cu, hd ** -0.5,
-                                                causal=False, plan=plan, out=o)
+                                                causal=False, plan=plan, out=o, head_dim=run.attn_head_dim)
 
     out = {"workload": "Qwen2.5-VL vision tower (public config, random init), one 4K image: grid (1, 154, 274), "
                        "42196 patches -> 10549 tokens",
@@ -545,7 +545,8 @@ def run_vision(reps: int = 5):
         pairs = sum((b - a) ** 2 for a, b in zip(cu_host, cu_host[1:]))
         tf = 4.0 * pairs * hd * h / (ms * 1e-3) / 1e12
         out[name] = {"ms": round(ms, 4), "sequences": len(cu_host) - 1, "work_items": plan.num_items,
-                     "useful_tflops": round(tf, 1), "frac_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+                     "kernel_head_dim": run.attn_head_dim, "tflops": round(tf, 1),
+                     "frac_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
     del vt, heads, o, qkv
     torch.cuda.empty_cache()
     return out

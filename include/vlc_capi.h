@@ -29,7 +29,7 @@ extern "C" {
 
 #define VLC_OK 0
 #define VLC_ERR_INVALID (-1)     /* null pointer, bad size, stride or alignment */
-#define VLC_ERR_UNSUPPORTED (-2) /* a shape the kernels do not implement (e.g. head_dim != 128) */
+#define VLC_ERR_UNSUPPORTED (-2) /* a shape the kernels do not implement (e.g. a head_dim other than 128 or 80) */
 #define VLC_ERR_WORKSPACE (-3)   /* workspace smaller than the plan requires */
 #define VLC_ERR_CAPACITY (-4)    /* host plan buffer too small */
 #define VLC_ERR_PLAN (-5)        /* plan does not match the call's shapes */
@@ -170,6 +170,13 @@ int vlc_attn_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
  *   device copy; plan_len its length.
  * workspace: device scratch of at least the planned workspace_bytes.
  * out: [total_q, num_heads_q, head_dim] bf16, row stride out_row_stride.
+ * head_dim: 128, or 80 in contiguous mode (the vision tower's heads,
+ *   flash_attn_varlen_func(..., causal=False) at models/qwen2_5_vl.py:200-210):
+ *   heads stay rows of 128 elements in q, k, v and out, the products read dims
+ *   0..79 of q and k and 0..95 of v; output dims 96..127 are zero and 80..95
+ *   hold P.V of v's dims 80..95 (zero when v is zero-padded, as
+ *   vlc_vision_rope_pad writes it).  The plan must be built with the same
+ *   head_dim.
  */
 int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride,
                         const void* k, int64_t k_row_stride,

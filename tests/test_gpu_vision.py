@@ -4,9 +4,10 @@
   same cos/sin tables), v copied, padding zero; the device cos/sin tables within
   one bf16 ulp of the oracle's (torch's cos/sin on host and device may round a
   near-tie differently);
-* window and whole-image attention through the padded 128-dim heads against
-  the fp32 oracle under the per-(row, head) bar, including every row of a
-  4K image's whole-image attention sampled at full size;
+* window and whole-image attention of the zero-padded 80-dim heads, through the
+  kernel's 128-dim path and its 80-dim path, against the fp32 oracle under the
+  per-(row, head) bar, including 96 rows of a 4K image's whole-image attention
+  at full size;
 * the whole tower against the fp32 oracle (with the reference's bf16 angles) on
   a tiny configuration and on the public 32-block configuration with small
   images; the bf16 product and the fp32 oracle differ by bf16 rounding through
@@ -100,36 +101,40 @@ def test_vision_rope_pad_refuses_bad_tables(dev):
                                 sin[:, :10].contiguous(), 16, 80)
 
 
+@pytest.mark.parametrize("hd", [128, 80], ids=["as-128", "hd80"])
 @pytest.mark.parametrize("full", [False, True], ids=["windows", "whole-image"])
-def test_padded_attention(dev, full):
+def test_padded_attention(dev, full, hd):
+    """80-dim heads in 128-element rows, through the kernel's 128-dim path (zero dims take
+    part in the products) and its 80-dim path (the products skip them)."""
     grids = [(1, 4, 4), (1, 20, 34), (2, 6, 10)]
-    say(f"vision: padded 80-dim attention, full={full}, grids={grids}")
+    say(f"vision: padded 80-dim attention, full={full}, kernel head_dim={hd}, grids={grids}")
     lay, qkv, cos, sin = _rope_inputs(dev, grids, seed=7)
     heads = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
     cu = lay.cu_full if full else lay.cu_window
-    plan = kernels.plan_attention(cu, cu, 16, 16, 128, False, dev)
+    plan = kernels.plan_attention(cu, cu, 16, 16, hd, False, dev)
     cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
     o = kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu_t, cu_t, 80 ** -0.5, causal=False,
-                                 plan=plan).cpu()
+                                 plan=plan, head_dim=hd).cpu()
     hc = heads.cpu()
     ref = oattn.varlen_attention(hc[:, 0, :, :80], hc[:, 1, :, :80], hc[:, 2, :, :80], cu, cu, 80 ** -0.5, False)
     assert_attn_close(o[..., :80], ref, what="padded vision attention")
     assert not o[..., 80:].view(torch.int16).any()
 
 
-def test_whole_image_attention_4k_sampled_rows(dev):
+@pytest.mark.parametrize("hd", [128, 80], ids=["as-128", "hd80"])
+def test_whole_image_attention_4k_sampled_rows(dev, hd):
     """Whole-image attention over a 4K image's 42196 patches at full size; 96 query rows
     (spread over the sequence, both ends included) against the fp32 oracle."""
     grids = [(1, 154, 274)]
-    say("vision: 4K whole-image attention, 42196 x 42196, non-causal")
+    say(f"vision: 4K whole-image attention, 42196 x 42196, non-causal, kernel head_dim={hd}")
     lay, qkv, cos, sin = _rope_inputs(dev, grids, seed=11)
     heads = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
     cu = lay.cu_full
-    plan = kernels.plan_attention(cu, cu, 16, 16, 128, False, dev)
+    plan = kernels.plan_attention(cu, cu, 16, 16, hd, False, dev)
     print(f"plan: items={plan.num_items} combines={plan.num_combine}", flush=True)
     cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
     o = kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu_t, cu_t, 80 ** -0.5, causal=False,
-                                 plan=plan).cpu()
+                                 plan=plan, head_dim=hd).cpu()
     hc = heads.cpu()
     n = lay.num_patches
     rows = torch.unique(torch.cat([torch.tensor([0, 1, n - 2, n - 1]), torch.linspace(0, n - 1, 92).long()]))
@@ -139,6 +144,22 @@ def test_whole_image_attention_4k_sampled_rows(dev):
     ref = torch.einsum("hrn,nhd->rhd", torch.softmax(s, dim=-1), v)
     assert_attn_close(o[rows, :, :80], ref, what="4K whole-image attention rows")
     assert np.isfinite(o.float().numpy()).all()
+
+
+def test_hd80_refuses_paged_calls_and_foreign_plans(dev):
+    lay, qkv, cos, sin = _rope_inputs(dev, [(1, 16, 16)])
+    heads = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
+    cu = lay.cu_window
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    plan128 = kernels.plan_attention(cu, cu, 16, 16, 128, False, dev)
+    with pytest.raises(ValueError, match="head_dim"):
+        kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu_t, cu_t, 0.1, causal=False,
+                                 plan=plan128, head_dim=80)
+    cache = torch.zeros(4, 256, 16, 128, dtype=torch.bfloat16, device=dev)
+    bt = torch.zeros(len(cu) - 1, 1, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError, match="head_dim"):
+        kernels.varlen_attention(heads[:, 0], cache, cache, cu_t, cu_t, 0.1, causal=False, block_table=bt,
+                                 head_dim=80)
 
 
 def _tower_check(dev, cfg, grids, seed, row_cos_min):

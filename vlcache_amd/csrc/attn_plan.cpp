@@ -59,7 +59,7 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
                                int64_t* plan_len, int64_t* workspace_bytes) {
   if (!cu_q || !cu_k || !plan_len || !workspace_bytes || num_seqs < 0) return VLC_ERR_INVALID;
   if (num_heads_q <= 0 || num_heads_kv <= 0 || num_heads_q % num_heads_kv != 0) return VLC_ERR_INVALID;
-  if (head_dim != kHeadDim) return VLC_ERR_UNSUPPORTED;
+  if (head_dim != kHeadDim && head_dim != kHeadDimNarrow) return VLC_ERR_UNSUPPORTED;
   const int group = num_heads_q / num_heads_kv;
   if (group > kCols) return VLC_ERR_UNSUPPORTED;
   const int ppt = kCols / group;

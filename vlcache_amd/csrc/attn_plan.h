@@ -6,7 +6,10 @@
 namespace vlc {
 namespace attn {
 
-constexpr int kHeadDim = 128;   // only head_dim supported by the MFMA kernel
+constexpr int kHeadDim = 128;   // head row length of q, k, v and out (elements)
+// The other head_dim the kernel computes: 80 active dims in 128-element head rows
+// (the vision tower's heads, zero-padded), contiguous K/V only.
+constexpr int kHeadDimNarrow = 80;
 constexpr int kTileK = 64;      // keys per LDS tile; split boundaries are multiples of it
 constexpr int kCols = 128;      // (query position, q head) columns per workgroup
 constexpr int kBlocksPerCU = 2; // attention workgroups resident per CU

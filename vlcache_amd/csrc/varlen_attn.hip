@@ -171,8 +171,16 @@ __device__ __forceinline__ float half_wave_max(float x) {
   return fmaxf(a, b);
 }
 
-template <int MODE>
+// KS: 16-dim steps of q.k (head_dim / 16); MB: 32-dim blocks of the output (head_dim / 32,
+// rounded up).  Heads are 128-element rows either way; with head_dim 80 (KS 5, MB 3) the
+// products skip dims 80..127 of q and k and 96..127 of v (output dims 96..127 are zero,
+// 80..95 take v's values there).
+template <int MODE, int KS = 8, int MB = 4>
 __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const Params p) {
+  static_assert(KS >= 1 && KS <= 8 && MB >= 1 && MB <= 4 && 2 * MB >= KS, "head_dim <= 128");
+  constexpr int NPV = 4 * MB;       // O^T += V^T P^T MFMAs per tile
+  constexpr int NQK = 2 * KS;       // S^T = K Q^T MFMAs per tile
+  constexpr int NU = NPV + NQK;     // units of a pipelined step
   __shared__ __attribute__((aligned(1024))) uint8_t k_buf0[kTileK * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t k_buf1[kTileK * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t v_buf0[kTileK * 256];
@@ -206,12 +214,12 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 
   // Q^T fragment (B operand of S^T = K Q^T): lane holds Q[col][16*kk + 8*hf .. +8].
   // Invalid columns load row 0 (always readable) and are zeroed.
-  bf16x8 qf[8];
+  bf16x8 qf[KS];
   {
     const uint16_t* qrow = p.q + (valid ? (int64_t)(q0 + qpos) * p.q_row_stride + (int64_t)head * kHeadDim : 0) +
                            8 * hf;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int kk = 0; kk < KS; ++kk) {
       u32x4v w = *reinterpret_cast<const u32x4v*>(qrow + 16 * kk);
       if (!valid) w = u32x4v{0u, 0u, 0u, 0u};
       qf[kk] = __builtin_bit_cast(bf16x8, w);
@@ -246,11 +254,11 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 
   // The eight K and eight V operand offsets of a step, kept in registers across
   // the tile loop (each is the lane's base offset XOR a constant).
-  uint32_t kofs[8], vofs[8];
+  uint32_t kofs[KS], vofs[2 * MB];
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) kofs[kk] = koff0 ^ (uint32_t)(kk << 5);
+  for (int kk = 0; kk < KS; ++kk) kofs[kk] = koff0 ^ (uint32_t)(kk << 5);
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
     vofs[2 * mb] = voff0 ^ ((uint32_t)mb << 6);
     vofs[2 * mb + 1] = voff0 ^ (((uint32_t)mb << 6) | 32u | 2048u);
   }
@@ -311,7 +319,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   float m_run = -INFINITY;           // running max, scaled to log2 units
   float l_run = 0.f;
 
-  // S^T = K Q^T of one tile (K from LDS): 16 operand reads, 16 MFMAs.
+  // S^T = K Q^T of one tile (K from LDS): NQK operand reads, NQK MFMAs.
   auto qk = [&](const uint8_t* kb_lds, f32x16 (&S)[2]) __attribute__((always_inline)) {
     const uint32_t kof = opaque(koff0);
 #pragma unroll
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 #pragma unroll
       for (int e = 0; e < 16; ++e) S[kb][e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+    for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const bf16x8 a = *reinterpret_cast<const bf16x8*>(kb_lds + kb * 32 * 256 + (kof ^ (kk << 5)));
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   auto order_qk = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
+    for (int i = 0; i < NQK - 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
@@ -340,7 +348,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   auto rescale = [&](float alpha) __attribute__((always_inline)) {
     if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[mb][e] *= alpha;
     }
@@ -370,25 +378,26 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u};
   };
 
-  // O^T += V^T P^T of the last tile, reads kAhead MFMAs ahead (sched groups: 0x008
-  // MFMA, 0x100 LDS read).
+  // O^T += V^T P^T of the last tile, reads a few MFMAs ahead (sched groups: 0x008
+  // MFMA, 0x100 LDS read).  MFMA j: dim block j % MB, 16-key chunk (j / MB) & 1, key
+  // block j / (2 MB).
   auto pv_last = [&](const uint8_t* v_rd) __attribute__((always_inline)) {
     const uint32_t vof = opaque(voff0);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint8_t* vr = v_rd + ((j >> 3) * 32 + 16 * ((j >> 2) & 1)) * 256;
-      const uint32_t mb = (uint32_t)(j & 3) << 6;
+    for (int j = 0; j < NPV; ++j) {
+      const int mbi = j % MB, ch = (j / MB) & 1, kb = j / (2 * MB);
+      const uint8_t* vr = v_rd + (kb * 32 + 16 * ch) * 256;
+      const uint32_t mb = (uint32_t)mbi << 6;
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ mb)));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s16x4*)(vr + (vof ^ (mb | 32u | 2048u))));
       const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pk[j >> 3][(j >> 2) & 1],
-                                                         o[j & 3], 0, 0, 0);
+      o[mbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pk[kb][ch], o[mbi], 0, 0, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-    for (int i = 0; i < 13; ++i) {
+    for (int i = 0; i < NPV - 3; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
@@ -401,8 +410,8 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   // buffer with P = 0, at t = n-1 they compute an S^T that is never used and load
   // zero rows.
   //
-  // Its instruction order is fixed by hand, in 32 units separated by
-  // sched_barrier: unit i issues MFMA i (PV for i < 16, QK after), the operand
+  // Its instruction order is fixed by hand, in NU units (32 for 128-dim heads)
+  // separated by sched_barrier: unit i issues MFMA i (PV for i < NPV, QK after), the operand
   // read of MFMA i + kAhead, one tile load (units 0..7) and a slice of the
   // softmax of tile t (mask and max in units 0..2, the new running max in unit
   // 3, one or two exp2 per unit after), so the VALU work fills the matrix pipe's
@@ -417,27 +426,28 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     const uint32_t lr = opaque(lrow0), lcn = opaque(lchunk0);
     const int rel = min(limit, k_end - 1) - kt - 4 * hf;  // MASKED: keys past rel are masked
 
-    bf16x8 op[32];
+    bf16x8 op[NU];
     auto read_op = [&](int j) __attribute__((always_inline)) {
-      if (j < 16) {  // V^T operand: key block j >> 3, 16-key chunk (j >> 2) & 1, dim block j & 3
-        const uint8_t* vr = v_rd + ((j >> 3) * 32 + 16 * ((j >> 2) & 1)) * 256;
+      if (j < NPV) {  // V^T operand: dim block j % MB, 16-key chunk (j / MB) & 1, key block j / (2 MB)
+        const int mbi = j % MB, ch = (j / MB) & 1, kb = j / (2 * MB);
+        const uint8_t* vr = v_rd + (kb * 32 + 16 * ch) * 256;
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(vr + vofs[2 * (j & 3)]));
+            (__attribute__((address_space(3))) s16x4*)(vr + vofs[2 * mbi]));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(vr + vofs[2 * (j & 3) + 1]));
+            (__attribute__((address_space(3))) s16x4*)(vr + vofs[2 * mbi + 1]));
         const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         op[j] = __builtin_bit_cast(bf16x8, w);
-      } else {  // K operand: head-dim step (j - 16) >> 1, key block (j - 16) & 1
-        const int kk = (j - 16) >> 1, kb = (j - 16) & 1;
+      } else {  // K operand: head-dim step (j - NPV) >> 1, key block (j - NPV) & 1
+        const int kk = (j - NPV) >> 1, kb = (j - NPV) & 1;
         op[j] = *reinterpret_cast<const bf16x8*>(k_rd + kb * 32 * 256 + kofs[kk]);
       }
     };
     auto mfma_op = [&](int j) __attribute__((always_inline)) {
-      if (j < 16) {
-        const int mb = j & 3;
-        o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[j], pk[j >> 3][(j >> 2) & 1], o[mb], 0, 0, 0);
+      if (j < NPV) {
+        const int mbi = j % MB, ch = (j / MB) & 1, kb = j / (2 * MB);
+        o[mbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[j], pk[kb][ch], o[mbi], 0, 0, 0);
       } else {
-        const int kk = (j - 16) >> 1, kb = (j - 16) & 1;
+        const int kk = (j - NPV) >> 1, kb = (j - NPV) & 1;
         const f32x16 zacc = {};
         s_nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[j], qf[kk], kk == 0 ? zacc : s_nxt[kb], 0, 0, 0);
       }
@@ -458,11 +468,15 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
       rs += pe;
     };
 
+    // exp2 slices: units 4 .. 4 + kTwo - 1 take two elements each, the rest one, so the
+    // 32 elements of the tile are spread over units 4 .. NU - 1.
+    constexpr int kTwo = 32 - (NU - 4);
+    static_assert(kTwo >= 0 && kTwo <= NU - 4, "the softmax slices must fit the step's units");
 #pragma unroll
     for (int j = 0; j < kAhead; ++j) read_op(j);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      if (i + kAhead < 32) read_op(i + kAhead);
+    for (int i = 0; i < NU; ++i) {
+      if (i + kAhead < NU) read_op(i + kAhead);
       mfma_op(i);
       if (MODE != kPagedRows) {
         // row (< 64) x row stride (< 2^24 bytes, checked on the host): a 24-bit multiply-add
@@ -499,11 +513,11 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
         m_base = (m_new == -INFINITY) ? 0.f : m_new;
         pin(m_base);
         pin(alpha);
-      } else if (i < 8) {  // two elements per unit, then one
+      } else if (i < 4 + kTwo) {  // two elements per unit, then one
         exp_elem(2 * (i - 4));
         exp_elem(2 * (i - 4) + 1);
       } else {
-        exp_elem(i);
+        exp_elem(2 * kTwo + (i - 4 - kTwo));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -721,7 +735,8 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
                                 int64_t workspace_bytes, void* stream) {
   using namespace vlc;
   using namespace vlc::attn;
-  if (head_dim != kHeadDim) return VLC_ERR_UNSUPPORTED;
+  if (head_dim != kHeadDim && head_dim != kHeadDimNarrow) return VLC_ERR_UNSUPPORTED;
+  if (head_dim == kHeadDimNarrow && block_table) return VLC_ERR_UNSUPPORTED;  // contiguous K/V only
   if (num_heads_q <= 0 || num_heads_kv <= 0 || num_heads_q % num_heads_kv != 0) return VLC_ERR_INVALID;
   if (!plan_host || !plan_dev || plan_len < kHeaderInts) return VLC_ERR_PLAN;
   const int32_t* h = plan_host;
@@ -787,7 +802,10 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
 
   hipStream_t s = as_stream(stream);
   const int mode = !block_table ? kContiguous : (page_size % kTileK == 0 ? kPagedTiles : kPagedRows);
-  if (mode == kContiguous)
+  if (head_dim == kHeadDimNarrow)
+    hipLaunchKernelGGL((attn_fwd_kernel<kContiguous, kHeadDimNarrow / 16, (kHeadDimNarrow + 31) / 32>),
+                       dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+  else if (mode == kContiguous)
     hipLaunchKernelGGL(attn_fwd_kernel<kContiguous>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
   else if (mode == kPagedTiles)
     hipLaunchKernelGGL(attn_fwd_kernel<kPagedTiles>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);

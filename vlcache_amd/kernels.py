@@ -14,6 +14,8 @@ import torch
 from . import _lib
 
 HEAD_DIM = 128  # the attention kernel's head dimension
+_PLAN_HEAD_DIM = 10  # header word of a vlc_attn_plan plan holding its head_dim
+ATTN_HEAD_DIMS = (128, 80)  # head_dims of vlc_varlen_attn_fwd (80: contiguous k/v only)
 
 
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
@@ -291,14 +293,17 @@ def _check_rows(name: str, t: torch.Tensor, heads: int) -> None:
 def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, softmax_scale: float,
                      causal: bool = True, block_table: torch.Tensor | None = None,
-                     plan: AttnPlan | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                     plan: AttnPlan | None = None, out: torch.Tensor | None = None,
+                     head_dim: int = HEAD_DIM) -> torch.Tensor:
     """Varlen GQA attention, paged (block_table given) or contiguous (vlc_varlen_attn_fwd).
 
     q: [total_q, Hq, 128] bf16.  Paged: k/v caches [num_blocks, page, Hkv, 128];
     contiguous: k/v [total_k, Hkv, 128] (v may be a strided view).  cu_seqlens_*:
     int32 device tensors.  plan: from plan_attention over the same host
-    boundaries; when None it is built here from a device-to-host copy of the
-    boundaries (a synchronisation).
+    boundaries (and head_dim); when None it is built here from a device-to-host
+    copy of the boundaries (a synchronisation).  head_dim 80 (contiguous only):
+    heads stay 128-element rows, the products use dims 0..79 of q and k and
+    0..95 of v (pass v zero-padded); output dims 96..127 are zero.
     """
     _require_device("varlen_attention", q, k, v, cu_seqlens_q, cu_seqlens_k, block_table)
     hq = q.shape[1]
@@ -325,11 +330,15 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         k_rs, v_rs = k.stride(0), v.stride(0)
         page, nblocks, bt_ptr, bt_rs = 0, 0, None, 0
+    if head_dim not in ATTN_HEAD_DIMS or (head_dim != HEAD_DIM and paged):
+        raise ValueError(f"head_dim {head_dim} is not supported (128, or 80 with contiguous k/v)")
     if plan is None:
-        plan = plan_attention(cu_seqlens_q.tolist(), cu_seqlens_k.tolist(), hq, hkv, HEAD_DIM, causal,
+        plan = plan_attention(cu_seqlens_q.tolist(), cu_seqlens_k.tolist(), hq, hkv, head_dim, causal,
                               q.device)
     if plan.num_seqs != num_seqs or plan.num_heads_q != hq or plan.num_heads_kv != hkv or plan.causal != bool(causal):
         raise ValueError("attention plan does not match the call")
+    if int(plan.host[_PLAN_HEAD_DIM]) != head_dim:
+        raise ValueError(f"attention plan was built for head_dim {int(plan.host[_PLAN_HEAD_DIM])}, the call has {head_dim}")
     # Bounds the kernel relies on, checked against the plan's host boundaries
     # (the device cu_seqlens must hold the same values).
     if plan.cu_seqlens_q[-1] > q.shape[0]:
@@ -346,7 +355,7 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     st = _lib.load().vlc_varlen_attn_fwd(
         q.data_ptr(), q.stride(0), k.data_ptr(), k_rs, v.data_ptr(), v_rs,
         bt_ptr, bt_rs, page, nblocks, cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
-        num_seqs, hq, hkv, HEAD_DIM, float(softmax_scale), 1 if causal else 0,
+        num_seqs, hq, hkv, head_dim, float(softmax_scale), 1 if causal else 0,
         plan.host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), plan.dev.data_ptr(), plan.host.size,
         out.data_ptr(), out.stride(0), ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0, _stream(q))

@@ -14,9 +14,9 @@ On gfx950:
     128-dim head rows run as one kernel (vlc_vision_rope_pad);
   * attention runs on the varlen attention kernel in its contiguous,
     non-causal mode (the reference calls flash_attn_varlen_func with
-    causal=False and cu_seqlens_q == cu_seqlens_k, :200-210); the 80-dim heads
-    are zero-padded to the kernel's 128 dims, which leaves q.k and the first 80
-    output dims unchanged; one work plan per boundary list serves every block;
+    causal=False and cu_seqlens_q == cu_seqlens_k, :200-210), in its 80-dim
+    variant: heads stay zero-padded 128-element rows, the products skip the
+    padding; one work plan per boundary list serves every block;
   * each RMSNorm (with its residual add) and the MLP's SiLU-and-multiply run
     as one kernel each; GEMMs and the merger's GELU run on torch (hipBLASLt).
 
@@ -135,7 +135,7 @@ class VisionAttention(nn.Module):
         heads = kernels.vision_rope_pad(qkv, run.pos_hw, run.cos, run.sin, self.num_heads, self.head_dim)
         cu, plan = (run.cu_full, run.plan_full) if full else (run.cu_window, run.plan_window)
         o = kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu, cu, self.head_dim ** -0.5,
-                                     causal=False, plan=plan)
+                                     causal=False, plan=plan, head_dim=run.attn_head_dim)
         return self.proj(o[..., :self.head_dim].reshape(n, self.num_heads * self.head_dim))
 
 
@@ -226,16 +226,16 @@ class VisionTransformer(nn.Module):
             return torch.tensor(cu, dtype=torch.int32, device=dev)
 
         cos, sin = self.rope_tables(lay.max_pos)
-        run = _Run(layout=lay,
+        # 80-dim heads have a kernel of their own; other widths run as zero-padded 128-dim heads
+        ahd = self.head_dim if self.head_dim in kernels.ATTN_HEAD_DIMS else kernels.HEAD_DIM
+        run = _Run(layout=lay, attn_head_dim=ahd,
                    patch_order=torch.from_numpy(lay.patch_order).to(dev),
                    reverse=torch.from_numpy(lay.reverse).to(dev),
                    pos_hw=torch.from_numpy(lay.pos_hw).to(dev),
                    cos=cos, sin=sin,
                    cu_window=cu_t(lay.cu_window), cu_full=cu_t(lay.cu_full),
-                   plan_window=kernels.plan_attention(lay.cu_window, lay.cu_window, h, h, kernels.HEAD_DIM,
-                                                      False, dev),
-                   plan_full=kernels.plan_attention(lay.cu_full, lay.cu_full, h, h, kernels.HEAD_DIM,
-                                                    False, dev))
+                   plan_window=kernels.plan_attention(lay.cu_window, lay.cu_window, h, h, ahd, False, dev),
+                   plan_full=kernels.plan_attention(lay.cu_full, lay.cu_full, h, h, ahd, False, dev))
         self._runs[key] = run
         while len(self._runs) > self._plan_cache:
             self._runs.popitem(last=False)
