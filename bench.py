@@ -469,6 +469,67 @@ def run_decode(reps: int = 10):
     }
 
 
+def run_decode_tail(steps: int = 128):
+    """The two-image 7B batch through the engine, then its decode tail.
+
+    Random-init Qwen2.5-VL-7B (28 text layers, 32-block vision tower).  Two cold
+    requests (64 text + image + 64 text, for a 1920x1080 and a 4K image of random
+    pixels) fill the encoder and image-KV caches; then 4 warm requests of 64 text +
+    1080p image + 64 text + 4K image + 64 text = 13432 tokens (ratio 0.02: 54 + 211
+    image tokens recomputed) generate `steps` tokens each (ignore_eos).  The
+    engine runs eagerly (no graph capture).  A warm-up batch of 8 tokens comes
+    first.  decode_ms_per_step = (wall time of the generate call - the latest first
+    token's TTFT) / (steps - 1): every step after the prefill is a decode step of
+    the batch of 4 at 13.4k-13.6k context.
+    """
+    import numpy as np
+
+    from vlcache_amd import LLM, SamplingParams
+    from vlcache_amd.config import QWEN25_VL_7B
+
+    img = QWEN25_VL_7B["image_token_id"]
+    llm = LLM(dict(QWEN25_VL_7B), recompute_ratio=0.02, num_kvcache_blocks=640, enforce_eager=True,
+              max_model_len=16384, max_num_batched_tokens=32768)
+    rng = np.random.default_rng(5)
+    g1, g2 = (1, 78, 138), (1, 154, 274)          # 39 x 69 = 2691 and 77 x 137 = 10549 tokens
+    n1, n2 = 39 * 69, 77 * 137
+    gen = torch.Generator().manual_seed(11)
+    p1 = torch.randn(g1[1] * g1[2], 1176, generator=gen)
+    p2 = torch.randn(g2[1] * g2[2], 1176, generator=gen)
+
+    def text(n):
+        return [int(x) for x in rng.integers(1, 150000, n)]
+
+    cold = [text(64) + [img] * n1 + text(64), text(64) + [img] * n2 + text(64)]
+    cold_mm = [{"pixel_values": p1, "image_grid_thw": torch.tensor([list(g1)])},
+               {"pixel_values": p2, "image_grid_thw": torch.tensor([list(g2)])}]
+    llm.generate(cold, SamplingParams(temperature=0.6, max_tokens=1), mm_inputs=cold_mm)
+    warm_mm = {"pixel_values": torch.cat([p1, p2]), "image_grid_thw": torch.tensor([list(g1), list(g2)])}
+
+    def batch():
+        return [text(64) + [img] * n1 + text(64) + [img] * n2 + text(64) for _ in range(4)]
+
+    llm.generate(batch(), SamplingParams(temperature=0.6, max_tokens=8, ignore_eos=True), mm_inputs=[warm_mm] * 4)
+    torch.cuda.synchronize()
+    prompts = batch()
+    t0 = time.perf_counter()
+    outs = llm.generate(prompts, SamplingParams(temperature=0.6, max_tokens=steps, ignore_eos=True),
+                        mm_inputs=[warm_mm] * 4)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ttft = max(o["ttft"] for o in outs)
+    assert all(len(o["token_ids"]) == steps for o in outs)
+    assert all(o["vit_time"] == 0.0 for o in outs), "warm requests must hit the encoder cache"
+    step_ms = (wall - ttft) * 1e3 / (steps - 1)
+    del llm
+    torch.cuda.empty_cache()
+    return {"workload": "Qwen2.5-VL-7B (random init), batch 4 x (64 + 2691 + 64 + 10549 + 64) tokens, ratio 0.02, "
+                        f"both images cached; {steps} tokens per request",
+            "warm_batch_ttft_ms": round(ttft * 1e3, 2), "decode_ms_per_step": round(step_ms, 3),
+            "decode_tokens_per_s": round(4 * 1e3 / step_ms, 1),
+            "timing": "engine wall clock (eager, no graph capture), after a cold pass and a warm-up batch"}
+
+
 def run_vision(reps: int = 5):
     """The vision tower on one 4K image (grid (1, 154, 274): 42196 patches -> 10549 tokens).
 
@@ -624,6 +685,7 @@ def main():
     ap.add_argument("--no-ttft", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-vision", action="store_true", help="skip the vision tower sub-result")
+    ap.add_argument("--no-decode-tail", action="store_true", help="skip the 7B batch's decode tail")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads' sub-results")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run one plain device-to-device copy of this many MiB (HBM counter calibration)")
@@ -647,6 +709,7 @@ def main():
     r = run_gpu(args.steps, args.warmup, args.workload)
     decode = run_decode() if not args.no_decode else None
     vision = run_vision() if not args.no_vision else None
+    decode_tail = run_decode_tail() if not args.no_decode_tail else None
     others = {}
     if not args.no_configs:
         for name, kw in (("cfg1", {"scatter": True}), ("cfg3", {"scatter": True}), ("cfg4", {}), ("cfg5", {})):
@@ -732,6 +795,7 @@ def main():
         "ms_per_step_graph": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
         "warm_ttft": ttft,
         "vision": vision,
+        "decode_tail": decode_tail,
         "configs": others,
     }
     print(json.dumps(line), flush=True)

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import numpy as np
+import torch
 import pytest
 
 from oracle import prefill as op
@@ -377,3 +378,25 @@ def test_runner_refuses_token_ids_outside_the_vocabulary():
     for bad in ([1, 151655], [-1, 3]):
         with pytest.raises(ValueError, match="outside the vocabulary"):
             ModelRunner._checked_ids(stub, np.array(bad))
+
+
+def test_image_hash_is_the_reference_digest():
+    """xxh64 over the grid's bytes then the pixel values' bytes, as
+    EncoderCacheManager.compute_hash (engine/encoder_cache_manager.py:25-29) computes it
+    from numpy's tobytes(); bf16 pixels hash their raw bytes."""
+    import xxhash
+
+    from vlcache_amd.engine.llm_engine import image_hash
+
+    pv = torch.randn(96, 1176, generator=torch.Generator().manual_seed(1))
+    grid = torch.tensor([1, 8, 12])
+    h = xxhash.xxh64()
+    h.update(grid.numpy().tobytes())
+    h.update(pv.numpy().tobytes())
+    assert image_hash(pv, grid) == h.intdigest()
+    assert image_hash(pv[:48], grid) != image_hash(pv[48:], grid)
+    b = pv.to(torch.bfloat16)
+    h2 = xxhash.xxh64()
+    h2.update(grid.numpy().tobytes())
+    h2.update(b.view(torch.int16).numpy().tobytes())
+    assert image_hash(b, grid) == h2.intdigest()

@@ -30,8 +30,9 @@ from .sequence import Sequence
 def image_hash(pixel_values: torch.Tensor, grid_thw: torch.Tensor) -> int:
     h = xxhash.xxh64()
     h.update(grid_thw.cpu().numpy().tobytes())
-    # raw bytes of any dtype (numpy has no bf16): the same bytes as numpy's tobytes() for fp32
-    h.update(pixel_values.detach().cpu().contiguous().view(torch.uint8).numpy().tobytes())
+    # raw bytes of any dtype (numpy has no bf16), hashed in place through the buffer
+    # protocol: the same digest as hashing numpy's tobytes() copy, without the copy
+    h.update(pixel_values.detach().cpu().contiguous().view(torch.uint8).numpy())
     return h.intdigest()
 
 
