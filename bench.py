@@ -476,11 +476,12 @@ def run_decode_tail(steps: int = 128):
     requests (64 text + image + 64 text, for a 1920x1080 and a 4K image of random
     pixels) fill the encoder and image-KV caches; then 4 warm requests of 64 text +
     1080p image + 64 text + 4K image + 64 text = 13432 tokens (ratio 0.02: 54 + 211
-    image tokens recomputed) generate `steps` tokens each (ignore_eos).  The
-    engine runs eagerly (no graph capture).  A warm-up batch of 8 tokens comes
-    first.  decode_ms_per_step = (wall time of the generate call - the latest first
-    token's TTFT) / (steps - 1): every step after the prefill is a decode step of
-    the batch of 4 at 13.4k-13.6k context.
+    image tokens recomputed) generate `steps` tokens each (ignore_eos), once with
+    the decode steps replaying captured HIP graphs (enforce_eager=False, the
+    reference's default) and once eagerly.  A warm-up batch of 8 tokens comes first
+    (it captures the batch-4 graph).  decode_ms_per_step = (wall time of the
+    generate call - the latest first token's TTFT) / (steps - 1): every step after
+    the prefill is a decode step of the batch of 4 at 13.4k-13.6k context.
     """
     import numpy as np
 
@@ -488,8 +489,9 @@ def run_decode_tail(steps: int = 128):
     from vlcache_amd.config import QWEN25_VL_7B
 
     img = QWEN25_VL_7B["image_token_id"]
-    llm = LLM(dict(QWEN25_VL_7B), recompute_ratio=0.02, num_kvcache_blocks=640, enforce_eager=True,
-              max_model_len=16384, max_num_batched_tokens=32768)
+    llm = LLM(dict(QWEN25_VL_7B), recompute_ratio=0.02, num_kvcache_blocks=640, enforce_eager=False,
+              max_model_len=16384, max_num_batched_tokens=32768, max_num_seqs=16)
+    runner = llm.model_runner
     rng = np.random.default_rng(5)
     g1, g2 = (1, 78, 138), (1, 154, 274)          # 39 x 69 = 2691 and 77 x 137 = 10549 tokens
     n1, n2 = 39 * 69, 77 * 137
@@ -510,24 +512,27 @@ def run_decode_tail(steps: int = 128):
         return [text(64) + [img] * n1 + text(64) + [img] * n2 + text(64) for _ in range(4)]
 
     llm.generate(batch(), SamplingParams(temperature=0.6, max_tokens=8, ignore_eos=True), mm_inputs=[warm_mm] * 4)
-    torch.cuda.synchronize()
-    prompts = batch()
-    t0 = time.perf_counter()
-    outs = llm.generate(prompts, SamplingParams(temperature=0.6, max_tokens=steps, ignore_eos=True),
-                        mm_inputs=[warm_mm] * 4)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ttft = max(o["ttft"] for o in outs)
-    assert all(len(o["token_ids"]) == steps for o in outs)
-    assert all(o["vit_time"] == 0.0 for o in outs), "warm requests must hit the encoder cache"
-    step_ms = (wall - ttft) * 1e3 / (steps - 1)
-    del llm
+    out = {"workload": "Qwen2.5-VL-7B (random init), batch 4 x (64 + 2691 + 64 + 10549 + 64) tokens, ratio 0.02, "
+                       f"both images cached; {steps} tokens per request"}
+    for mode, eager in (("graphs", False), ("eager", True)):
+        runner.enforce_eager = eager
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outs = llm.generate(batch(), SamplingParams(temperature=0.6, max_tokens=steps, ignore_eos=True),
+                            mm_inputs=[warm_mm] * 4)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ttft = max(o["ttft"] for o in outs)
+        assert all(len(o["token_ids"]) == steps for o in outs)
+        assert all(o["vit_time"] == 0.0 for o in outs), "warm requests must hit the encoder cache"
+        step_ms = (wall - ttft) * 1e3 / (steps - 1)
+        out[mode] = {"warm_batch_ttft_ms": round(ttft * 1e3, 2), "decode_ms_per_step": round(step_ms, 3),
+                     "decode_tokens_per_s": round(4 * 1e3 / step_ms, 1)}
+    out["timing"] = ("engine wall clock after a cold pass and a warm-up batch; 'graphs': decode steps replay "
+                     "captured HIP graphs, 'eager': the same engine with graph replay off")
+    del llm, runner
     torch.cuda.empty_cache()
-    return {"workload": "Qwen2.5-VL-7B (random init), batch 4 x (64 + 2691 + 64 + 10549 + 64) tokens, ratio 0.02, "
-                        f"both images cached; {steps} tokens per request",
-            "warm_batch_ttft_ms": round(ttft * 1e3, 2), "decode_ms_per_step": round(step_ms, 3),
-            "decode_tokens_per_s": round(4 * 1e3 / step_ms, 1),
-            "timing": "engine wall clock (eager, no graph capture), after a cold pass and a warm-up batch"}
+    return out
 
 
 def run_vision(reps: int = 5):

@@ -339,3 +339,49 @@ def test_two_image_warm_request_equals_full_recompute_for_same_context(dev):
     full = _engine(0.0)
     _, lf = _prefill_logits(full, toks_b, mm)
     assert_close(lw, lf, atol=5e-2, cos_min=0.999, what="two-image warm vs full logits (same context)")
+
+
+def test_decode_graph_replays_match_the_eager_decode(dev):
+    """enforce_eager=False: decode steps replay captured HIP graphs.  Three requests (one
+    with an image, one long enough to span blocks) are prefilled, then for 5 decode steps
+    the eager decode forward and the graph replay (batch 3 padded to the captured size 4)
+    are run on the same step; the logits agree under the cosine bar (the GEMMs of a
+    4-row and a 3-row batch may round differently, and the graph's decode plan covers
+    max_model_len), every replay after eager work and synchronisation.  The batch shrinks
+    3 -> 2 -> 1 as requests finish, so three captured sizes (4, 2, 1) replay."""
+    from vlcache_amd import LLM
+    from vlcache_amd.utils.context import reset_context
+
+    say("engine: decode HIP graphs vs eager decode, 5 steps, batches 3 (bucket 4), 2, 1")
+    eng = LLM(dict(TINY), recompute_ratio=0.1, num_kvcache_blocks=16, max_model_len=2048, seed=3,
+              synthetic_vision=True, enforce_eager=False, max_num_seqs=8)
+    runner = eng.model_runner
+    rng = np.random.default_rng(1)
+    toks_img, mm = _request(20, (1, 8, 8), 12, 4)
+    prompts = [toks_img, [int(x) for x in rng.integers(1, 900, 300)], [int(x) for x in rng.integers(1, 900, 40)]]
+    mms = [mm, None, None]
+    sps = [SamplingParams(temperature=1.0, max_tokens=6, ignore_eos=True),
+           SamplingParams(temperature=1.0, max_tokens=4, ignore_eos=True),
+           SamplingParams(temperature=1.0, max_tokens=2, ignore_eos=True)]
+    for p, sp, m in zip(prompts, sps, mms):
+        eng.add_request(p, sp, m)
+    seqs, is_prefill = eng.scheduler.schedule()
+    assert is_prefill
+    tok = runner.run(seqs, True)[0]
+    eng.scheduler.postprocess(seqs, tok)
+    seen = set()
+    for step in range(5):
+        seqs, is_prefill = eng.scheduler.schedule()
+        assert not is_prefill
+        with torch.inference_mode():
+            ids, pos = runner.prepare_decode(seqs)
+            le = runner.run_model(ids, pos, False)[0].float().cpu()
+            reset_context()
+            torch.cuda.synchronize()
+            lg = runner._run_decode_graph(seqs).float().cpu()
+            reset_context()
+        seen.add(len(seqs))
+        assert_close(lg, le, atol=5e-2, cos_min=0.9999, what=f"decode step {step}, batch {len(seqs)}")
+        eng.scheduler.postprocess(seqs, le.argmax(-1).tolist())
+    assert seen == {1, 2, 3}, seen
+    assert set(runner._graphs) == {1, 2, 4}

@@ -24,16 +24,16 @@ inline int launch_status() {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// bf16 <-> fp32 by bit manipulation (round to nearest even, NaN kept quiet).
+// bf16 <-> fp32.  bf16 -> fp32 is a shift; fp32 -> bf16 rounds to nearest even with
+// the hardware conversion (v_cvt_pk_bf16_f32; NaN stays NaN), which measured about
+// twice as fast as the same rounding done with integer operations in the
+// instruction-bound RMSNorm and rotation kernels.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 }  // namespace vlc

@@ -24,10 +24,13 @@ constexpr int kRowsPerBlock = kThreads / 64;
 
 __device__ __forceinline__ float lo16(uint32_t w) { return bf16_bits_to_f32(w & 0xffffu); }
 __device__ __forceinline__ float hi16(uint32_t w) { return bf16_bits_to_f32(w >> 16); }
-__device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+// fp32 -> bf16 with the hardware conversion (round to nearest even, v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ float rbf(float f) { return static_cast<float>(static_cast<__bf16>(f)); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -44,17 +47,30 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
+  // Every load of the row is issued before the first store: the new residual may be
+  // written over x or the old residual, so a store ahead of a later chunk's load would
+  // keep that load from being hoisted and serialise the row into CPL round trips.
+  // The weight chunks are loaded with them, so the scaling does not wait for a second
+  // round trip after the row's reduction.
+  u32x4 xa[CPL], ra[CPL], wa[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) {
+      xa[i] = *reinterpret_cast<const u32x4*>(x + row * x_stride_b + c * 16);
+      if constexpr (kResidual) ra[i] = *reinterpret_cast<const u32x4*>(res + row * res_stride_b + c * 16);
+      wa[i] = *reinterpret_cast<const u32x4*>(weight + c * 16);
+    }
+  }
   float s[CPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = lane + 64 * i;
     if (c < chunks) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(x + row * x_stride_b + c * 16);
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+      const uint32_t aw[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
       if constexpr (kResidual) {
-        const u32x4 b = *reinterpret_cast<const u32x4*>(res + row * res_stride_b + c * 16);
-        const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+        const uint32_t bw[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
         uint32_t ro[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -80,8 +96,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(
   for (int i = 0; i < CPL; ++i) {
     const int c = lane + 64 * i;
     if (c < chunks) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(weight + c * 16);
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      const uint32_t ww[4] = {wa[i].x, wa[i].y, wa[i].z, wa[i].w};
       uint32_t o[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)

@@ -82,6 +82,10 @@ class ModelRunner:
         self._logit_indices = None
         self._decode_plans: dict = {}
         self._decode_workspace = None
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._graph_vars = None
+        self._graph_host = None
+        self._graph_pool = None
         self.allocate_kv_cache()
 
     def call(self, method_name, *args):
@@ -232,7 +236,10 @@ class ModelRunner:
         self._logit_indices = logit_indices if has_partial else None
         return input_ids, positions, (mm if has_mm else None)
 
-    def prepare_decode(self, seqs: list[Sequence]):
+    def _decode_host_arrays(self, seqs: list[Sequence]):
+        """Host inputs of a decode step (engine/model_runner.py:322-338): last token ids,
+        positions (M-RoPE rows when used), the new token's slot, context lengths and the
+        block tables padded with -1."""
         n = len(seqs)
         input_ids = self._checked_ids(np.array([s.last_token for s in seqs], dtype=np.int64))
         lens = np.array([len(s) for s in seqs], dtype=np.int64)
@@ -245,6 +252,11 @@ class ModelRunner:
         bt = np.full((n, width), -1, dtype=np.int32)
         for i, s in enumerate(seqs):
             bt[i, :len(s.block_table)] = s.block_table
+        return input_ids, pos, slot, lens, bt
+
+    def prepare_decode(self, seqs: list[Sequence]):
+        n = len(seqs)
+        input_ids, pos, slot, lens, bt = self._decode_host_arrays(seqs)
         cu_q = list(range(n + 1))
         cu_k = [0] + np.cumsum(lens).tolist()
         plan = dplan = None
@@ -277,6 +289,7 @@ class ModelRunner:
             if plan.workspace_bytes > self._decode_workspace.numel():  # contexts beyond max_model_len
                 self._decode_workspace = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device=self.device)
                 self._decode_plans.clear()
+                self._graphs.clear()  # captured graphs hold the old workspace's address
             plan.workspace = self._decode_workspace
             if len(self._decode_plans) > 4096:
                 self._decode_plans.clear()
@@ -359,6 +372,102 @@ class ModelRunner:
                     out[i] = emb if r <= 0 else emb[:r]
         return (torch.cat(out, dim=0) if out else None), vit_time
 
+    # ------------------------------------------------------------------ decode graphs
+    # With enforce_eager=False a decode step replays a HIP graph of the model's decode
+    # forward, as the reference replays CUDA graphs (engine/model_runner.py:418-432,
+    # 453-479): inputs go into static buffers sized for the largest batch, the graph of
+    # the smallest captured batch size >= the step's batch replays, the logits are
+    # computed from its output rows.  Graphs are captured on first use of a batch size
+    # (1, 2, 4, 8, then multiples of 16 up to min(max_num_seqs, 512)), all in one memory
+    # pool.  Every kernel of the forward takes its inputs from device memory: the token
+    # ids, positions, slots, context lengths and block tables of the static buffers,
+    # and one decode launch plan per batch size that covers max_model_len (its shared
+    # workspace's counters return to zero after each call).  Padding rows carry slot -1
+    # (not stored) and context length 0 (zero output).
+    def _graph_buckets(self) -> list[int]:
+        top = min(self.config.max_num_seqs, 512)
+        return [b for b in (1, 2, 4, 8) if b <= top] + list(range(16, top + 1, 16))
+
+    def _graph_decode_ok(self, n: int) -> bool:
+        return (not self.enforce_eager and n <= self._graph_buckets()[-1] and
+                kernels.decode_supported(self.num_heads, self.num_kv_heads, self.head_dim, self.block_size))
+
+    def _graph_static(self):
+        if self._graph_vars is None:
+            mb = self._graph_buckets()[-1]
+            width = -(-self.config.max_model_len // self.block_size)
+            dev = self.device
+            rows = 3 if self.config.use_mrope else 1
+            self._graph_vars = dict(
+                input_ids=torch.zeros(mb, dtype=torch.int64, device=dev),
+                positions=torch.zeros(rows, mb, dtype=torch.int64, device=dev),
+                slot_mapping=torch.full((mb,), -1, dtype=torch.int32, device=dev),
+                context_lens=torch.zeros(mb, dtype=torch.int32, device=dev),
+                block_tables=torch.full((mb, width), -1, dtype=torch.int32, device=dev),
+                outputs=torch.zeros(mb, self.config.hf_config.hidden_size, dtype=self.dtype, device=dev))
+            self._graph_host = {k: torch.empty(v.shape, dtype=v.dtype, pin_memory=True)
+                                for k, v in self._graph_vars.items() if k != "outputs"}
+            self._graph_pool = torch.cuda.graph_pool_handle()
+        return self._graph_vars
+
+    def _graph_context(self, bs: int):
+        gv = self._graph_static()
+        cap = -(-max(self.config.max_model_len, 1) // 1024) * 1024
+        set_context(False, None, None, 1, cap, gv["slot_mapping"][:bs], gv["context_lens"][:bs],
+                    gv["block_tables"][:bs], decode_plan=self._decode_plan(bs, cap))
+
+    def _graph_positions(self, bs: int):
+        pos = self._graph_static()["positions"][:, :bs]
+        return pos if self.config.use_mrope else pos[0]
+
+    def _capture_decode_graph(self, bs: int):
+        gv = self._graph_static()
+        self._graph_context(bs)
+        ids, pos = gv["input_ids"][:bs], self._graph_positions(bs)
+        # one eager run on the capture inputs (padding state: nothing stored, empty contexts)
+        gv["outputs"][:bs] = self.model(ids, pos)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, self._graph_pool):
+            gv["outputs"][:bs] = self.model(ids, pos)
+        torch.cuda.synchronize(self.device)
+        reset_context()
+        self._graphs[bs] = g
+        return g
+
+    def _run_decode_graph(self, seqs: list[Sequence]) -> torch.Tensor:
+        n = len(seqs)
+        bs = next(b for b in self._graph_buckets() if b >= n)
+        input_ids, pos, slot, lens, bt = self._decode_host_arrays(seqs)
+        gv = self._graph_static()
+        g = self._graphs.get(bs)
+        if g is None:
+            g = self._capture_decode_graph(bs)
+        width = gv["block_tables"].shape[1]
+        if bt.shape[1] > width:
+            raise ValueError(f"a sequence needs {bt.shape[1]} blocks, more than max_model_len allows ({width})")
+        # Fill the pinned host mirrors of the static buffers (padding rows included), then
+        # copy each mirror's first bs rows up; the previous step's copies are done (its
+        # sampled tokens were read back), so the mirrors are free to overwrite.
+        hv = self._graph_host
+        rows = gv["positions"].shape[0]
+        hv["input_ids"][:bs] = 0
+        hv["input_ids"][:n] = torch.from_numpy(input_ids)
+        hv["positions"][:, :bs] = 0
+        hv["positions"][:, :n] = torch.from_numpy(pos.reshape(rows, n))
+        hv["slot_mapping"][:bs] = -1
+        hv["slot_mapping"][:n] = torch.from_numpy(slot.astype(np.int32))
+        hv["context_lens"][:bs] = 0
+        hv["context_lens"][:n] = torch.from_numpy(lens.astype(np.int32))
+        hv["block_tables"][:bs] = -1
+        hv["block_tables"][:n, :bt.shape[1]] = torch.from_numpy(bt)
+        for key in ("input_ids", "slot_mapping", "context_lens", "block_tables"):
+            gv[key][:bs].copy_(hv[key][:bs], non_blocking=True)
+        gv["positions"][:, :bs].copy_(hv["positions"][:, :bs], non_blocking=True)
+        g.replay()
+        set_context(False)
+        return self.model.compute_logits(gv["outputs"][:n])
+
     # ------------------------------------------------------------------ execution
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_prefill, mm=None):
@@ -368,6 +477,12 @@ class ModelRunner:
 
     @torch.inference_mode()
     def run(self, seqs: list[Sequence], is_prefill: bool):
+        if not is_prefill and self._graph_decode_ok(len(seqs)):
+            temperatures = self.prepare_sample(seqs)
+            logits = self._run_decode_graph(seqs)
+            token_ids = self.sampler(logits, temperatures).tolist()
+            reset_context()
+            return token_ids, 0.0
         if is_prefill:
             input_ids, positions, mm = self.prepare_prefill(seqs)
         else:
