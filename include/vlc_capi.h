@@ -328,6 +328,23 @@ int vlc_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int6
 int vlc_silu_mul(const void* gate_up, int64_t gate_up_row_stride, int64_t num_rows, int64_t inter,
                  void* out, int64_t out_row_stride, void* stream);
 
+/*
+ * Skinny linear layer (M <= 16 rows): out[m][n] = bf16(sum_k x[m][k] * weight[n][k] + bias[n]),
+ * fp32 accumulation.  Replaces the decode-step projections of the decoder
+ * (QKVParallelLinear / RowParallelLinear / MergedColumnParallelLinear and the LM head,
+ * models/qwen3.py:71-110, layers/embed_head.py:56-66) whose work is streaming the
+ * weights once.
+ *
+ * x: [rows, in_features] bf16 at x_row_stride; weight: [out_features, in_features]
+ * bf16 at w_row_stride (nn.Linear layout); bias: bf16 [out_features] or NULL;
+ * out: [rows, out_features] bf16 at out_row_stride.  rows <= 16, in_features % 32 == 0,
+ * out_features % 16 == 0; x and weight 16-byte aligned with row strides multiples of 8
+ * elements; out and bias 8-byte aligned, out_row_stride a multiple of 4.
+ */
+int vlc_linear_skinny(const void* x, int64_t x_row_stride, int64_t rows, int64_t in_features,
+                      const void* weight, int64_t w_row_stride, int64_t out_features, const void* bias,
+                      void* out, int64_t out_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,3 +89,56 @@ def test_silu_mul_extremes(dev):
     u = torch.tensor([[3.0, 2.0, 5.0, 1.0]]).to(torch.bfloat16)
     out = kernels.silu_mul(torch.cat([g, u], 1).to(dev)).float().cpu()
     assert out.tolist() == [[-0.0, 200.0, 0.0, -0.0]]
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(1, 32, 16, False), (3, 2048, 2560, True), (4, 3584, 4608, True),
+                                        (4, 18944, 3584, False), (16, 3584, 37888, False), (7, 11008, 2048, False),
+                                        (2, 2048, 151936, False)])
+def test_linear_skinny(dev, m, k, n, bias):
+    """vlc_linear_skinny against the fp32 product of the same bf16 operands, rounded once:
+    within one bf16 ulp of the fp32 reference (the fp32 sums are accumulated in another
+    order than the reference's, a relative change of about K * 2^-24)."""
+    from vlcache_amd import kernels
+
+    say(f"linear_skinny m={m} k={k} n={n} bias={bias}")
+    x = randn_bf16((m, k), m + k)
+    w = randn_bf16((n, k), n + k, 0.05)
+    b = randn_bf16((n,), 9) if bias else None
+    out = kernels.linear_skinny(x.to(dev), w.to(dev), b.to(dev) if bias else None).float().cpu()
+    ref = x.float() @ w.float().t() + (b.float() if bias else 0.0)
+    tol = ref.abs() * 2.0 ** -7 + ref.abs().max() * k * 2.0 ** -24
+    bad = int(((out - ref).abs() > tol).sum())
+    assert bad == 0, f"{bad} outputs beyond one bf16 ulp"
+    exact = float((out == ref.to(torch.bfloat16).float()).float().mean())
+    print(f"equal to the rounded fp32 reference: {exact:.4f}", flush=True)
+
+
+def test_linear_skinny_strided_rows_and_refusals(dev):
+    from vlcache_amd import kernels
+
+    big = randn_bf16((4, 3 * 1024), 3)
+    w = randn_bf16((256, 1024), 4)
+    x = big.to(dev)[:, 1024:2048]              # row stride 3072
+    out = kernels.linear_skinny(x, w.to(dev)).float().cpu()
+    ref = big[:, 1024:2048].float() @ w.float().t()
+    assert ((out - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-3).all()
+    with pytest.raises(ValueError):
+        kernels.linear_skinny(randn_bf16((17, 1024), 5).to(dev), w.to(dev))      # more than 16 rows
+    with pytest.raises(ValueError):
+        kernels.linear_skinny(randn_bf16((4, 1000), 5).to(dev), randn_bf16((256, 1000), 6).to(dev))  # K % 32
+
+
+def test_linear_layer_routes_few_rows_to_the_skinny_kernel(dev):
+    """layers.linear.Linear: <= 16 rows through vlc_linear_skinny, more through torch; both
+    agree with the fp32 product within bf16 rounding."""
+    from vlcache_amd.layers.linear import Linear
+
+    torch.manual_seed(0)
+    lin = Linear(2048, 512, bias=True).to(dev, torch.bfloat16)
+    for rows in (1, 16, 17, 300):
+        x = randn_bf16((rows, 2048), rows).to(dev)
+        y = lin(x).float().cpu()
+        ref = x.float().cpu() @ lin.weight.float().cpu().t() + lin.bias.float().cpu()
+        assert ((y - ref).abs() <= ref.abs() * 2.0 ** -6 + 2e-3).all(), rows
+    y3 = lin(randn_bf16((2, 3, 2048), 7).to(dev))
+    assert y3.shape == (2, 3, 512)

@@ -50,6 +50,7 @@ SIGNATURES = {
     "vlc_vision_rope_pad": (i32, [vp, i64, vp, vp, vp, i64, i64, i32, i32, i32, vp, i64, vp]),
     "vlc_rms_norm": (i32, [vp, i64, vp, i64, vp, i64, vp, f32, i64, i64, vp, i64, vp]),
     "vlc_silu_mul": (i32, [vp, i64, i64, i64, vp, i64, vp]),
+    "vlc_linear_skinny": (i32, [vp, i64, i64, i64, vp, i64, i64, vp, vp, i64, vp]),
     "vlc_attn_plan": (
         i32,
         [c_i32p, c_i32p, i32, i32, i32, i32, i32, i32, c_i32p, i64, c_i64p, c_i64p],

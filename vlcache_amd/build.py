@@ -22,7 +22,7 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
 
 HIP_SOURCES = ["store_kvcache.hip", "rope_store_kv.hip", "rerotate_kv.hip", "varlen_attn.hip", "decode_attn.hip",
-               "vision_rope.hip", "norm_act.hip"]
+               "vision_rope.hip", "norm_act.hip", "linear_skinny.hip"]
 HOST_SOURCES = ["attn_plan.cpp", "capi.cpp"]
 
 # Device flags: gfx950 only; packed-fp32 instructions are disabled for all HIP code.

@@ -608,3 +608,42 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Te
                                   _stream(gate_up))
     _lib.check("vlc_silu_mul", st)
     return o.view(*lead, inter)
+
+
+# --------------------------------------------------------------------------- skinny linear
+SKINNY_MAX_ROWS = 16
+
+
+def linear_skinny_supported(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> bool:
+    """Whether vlc_linear_skinny takes this call (bf16, at most 16 rows, K % 32, N % 16, aligned rows)."""
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.dim() == 2):
+        return False
+    m, k = x.shape
+    n = weight.shape[0]
+    if m > SKINNY_MAX_ROWS or k % 32 or n % 16 or weight.shape[1] != k:
+        return False
+    if x.stride(1) != 1 or weight.stride(1) != 1 or x.stride(0) % 8 or weight.stride(0) % 8:
+        return False
+    if x.data_ptr() % 16 or weight.data_ptr() % 16:
+        return False
+    if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous() or bias.data_ptr() % 8):
+        return False
+    return True
+
+
+def linear_skinny(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [M <= 16, K] @ weight[N, K]^T + bias (vlc_linear_skinny): the decode-step projections,
+    weight-streaming on the matrix pipe; fp32 accumulation, one rounding to bf16."""
+    _require_device("linear_skinny", x, weight, bias, out)
+    if not linear_skinny_supported(x, weight, bias):
+        raise ValueError(f"linear_skinny does not take x {tuple(x.shape)} / weight {tuple(weight.shape)}")
+    m, k = x.shape
+    n = weight.shape[0]
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    st = _lib.load().vlc_linear_skinny(x.data_ptr(), x.stride(0), m, k, weight.data_ptr(), weight.stride(0), n,
+                                       bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0),
+                                       _stream(x))
+    _lib.check("vlc_linear_skinny", st)
+    return out

@@ -6,7 +6,8 @@ Qwen2.5-VL variant: QKV bias, no q/k norm) and of
 Qwen2_5_VLForConditionalGeneration.forward (models/qwen2_5_vl.py:562-580: the
 image-token rows of the embeddings are replaced by visual embeddings).
 
-GEMMs stay on torch (hipBLASLt) and run eagerly; per layer the rotary
+GEMMs run on torch (hipBLASLt) except calls of at most 16 rows (decode steps),
+which stream the weights through vlc_linear_skinny (layers.linear.Linear); per layer the rotary
 embedding of q and k and the KV store run as one gfx950 kernel and the
 attention as another (layers.attention.Attention), each RMSNorm (with its
 residual add) as one kernel and the MLP's SiLU-and-multiply as one.
@@ -24,6 +25,7 @@ from torch import nn
 from . import kernels
 from .layers.attention import Attention
 from .layers.layernorm import RMSNorm
+from .layers.linear import Linear
 from .layers.rotary_embedding import get_rope
 from .utils.context import get_context
 from .vision import VisionTransformer, vision_config
@@ -43,8 +45,8 @@ class DecoderAttention(nn.Module):
         self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
         self.q_size = self.num_heads * self.head_dim
         self.kv_size = self.num_kv_heads * self.head_dim
-        self.qkv_proj = nn.Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=True)
-        self.o_proj = nn.Linear(self.q_size, cfg.hidden_size, bias=False)
+        self.qkv_proj = Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=True)
+        self.o_proj = Linear(self.q_size, cfg.hidden_size, bias=False)
         self.rotary_emb = get_rope(self.head_dim, self.head_dim, cfg.max_position_embeddings,
                                    getattr(cfg, "rope_theta", 1e6), getattr(cfg, "rope_scaling", None))
         self.attn = Attention(self.num_heads, self.head_dim, self.head_dim ** -0.5, self.num_kv_heads)
@@ -68,8 +70,8 @@ class MLP(nn.Module):
     def __init__(self, cfg):
         super().__init__()
         self.inter = cfg.intermediate_size
-        self.gate_up_proj = nn.Linear(cfg.hidden_size, 2 * cfg.intermediate_size, bias=False)
-        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+        self.gate_up_proj = Linear(cfg.hidden_size, 2 * cfg.intermediate_size, bias=False)
+        self.down_proj = Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x):
         return self.down_proj(kernels.silu_mul(self.gate_up_proj(x)))
@@ -119,7 +121,7 @@ class Qwen2_5_VLForConditionalGeneration(nn.Module):
         self.visual = (VisionTransformer(vision_config(vcfg, cfg.hidden_size), eps=cfg.rms_norm_eps)
                        if vcfg is not None else None)
         self.model = TextModel(cfg)
-        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+        self.lm_head = Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
         if getattr(cfg, "tie_word_embeddings", False):
             self.lm_head.weight = self.model.embed_tokens.weight
 
