@@ -92,10 +92,13 @@ def _mean_ms(evs):
 
 def _graph_us_per_call(fn_layer, num_layers: int, steps: int):
     """GPU time of one call of fn_layer(layer), averaged over the layers: the
-    num_layers calls are captured in one HIP graph, replayed `steps` times with
-    events around each replay.  Host time (the Python wrappers, event records) is
-    not in the figure; the launch gaps between the kernels are.  None if the
-    calls cannot be captured."""
+    num_layers calls (repeated until the graph holds at least 36, so that the
+    replay's own launch latency is spread over as many calls as a 36-layer step
+    has) are captured in one HIP graph, replayed `steps` times with events around
+    each replay.  Host time (the Python wrappers, event records) is not in the
+    figure; the launch gaps between the kernels are.  None if the calls cannot be
+    captured."""
+    reps = max(1, -(-36 // num_layers))
     try:
         st = torch.cuda.Stream()
         st.wait_stream(torch.cuda.current_stream())
@@ -105,8 +108,9 @@ def _graph_us_per_call(fn_layer, num_layers: int, steps: int):
         torch.cuda.current_stream().wait_stream(st)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for layer in range(num_layers):
-                fn_layer(layer)
+            for _ in range(reps):
+                for layer in range(num_layers):
+                    fn_layer(layer)
         g.replay()
         torch.cuda.synchronize()
         ev = _events(steps)
@@ -115,7 +119,7 @@ def _graph_us_per_call(fn_layer, num_layers: int, steps: int):
             g.replay()
             b.record()
         torch.cuda.synchronize()
-        return _mean_ms(ev) * 1e3 / num_layers
+        return _mean_ms(ev) * 1e3 / (num_layers * reps)
     except Exception as e:  # report, do not hide
         print(f"graph timing unavailable: {e!r}", file=sys.stderr)
         return None
