@@ -194,6 +194,16 @@ def test_tower_public_config_small_images(dev):
     _tower_check(dev, REAL, grids, 5, 0.999)
 
 
+def test_tower_two_frame_video(dev):
+    """A two-frame grid (t = 2): frames share the patch positions, windows are per frame,
+    the whole-image blocks attend over both frames (the reference's one sequence per
+    image, models/qwen2_5_vl.py:494-503); bar: per-row cosine >= 0.9995 against the
+    fp32 oracle."""
+    grids = [(2, 8, 12), (1, 4, 6)]
+    say(f"vision tower, tiny config, video grid {grids}")
+    _tower_check(dev, TINY, grids, 13, 0.9995)
+
+
 def test_tower_batch_equals_single_images(dev):
     """Images batched into one call give each image's own embeddings (windows and whole-image
     sequences never cross images); GEMMs may round differently at another row count, so
@@ -241,3 +251,20 @@ def test_engine_runs_the_tower_on_a_cold_image(dev):
     assert torch.equal(cache.get(h).view(torch.int16), direct.view(torch.int16))
     warm = llm.generate([toks(128, 16)], sp, mm_inputs=[mm])[0]
     assert warm["vit_time"] == 0.0 and cache.hits >= 2
+    # Two cold images in one request, one of them repeated by a second request in the same
+    # batch: one tower call over the distinct images; each image's rows equal a direct call.
+    g2 = (1, 8, 12)
+    pix2 = _pixels([g2], 22)
+    toks2 = ([int(x) for x in rng.integers(1, 150000, 20)] + [151655] * (4 * 6) +
+             [int(x) for x in rng.integers(1, 150000, 10)] + [151655] * n_img)
+    pix3 = _pixels([grid], 23)
+    mm2 = {"pixel_values": torch.cat([pix2, pix3]), "image_grid_thw": torch.tensor([list(g2), list(grid)])}
+    toks3 = [int(x) for x in rng.integers(1, 150000, 30)] + [151655] * (4 * 6) + [7]
+    mm3 = {"pixel_values": pix2, "image_grid_thw": torch.tensor([list(g2)])}
+    before = len(cache)
+    outs = llm.generate([toks2, toks3], sp, mm_inputs=[mm2, mm3])
+    assert all(o["vit_time"] > 0 for o in outs) and len(cache) == before + 2
+    keys = list(cache._entries)[-2:]
+    for key, (pv, g) in zip(keys, ((pix2, g2), (pix3, grid))):
+        direct = runner.model.visual(pv.to(dev), [g])
+        assert torch.equal(cache.get(key).view(torch.int16), direct.view(torch.int16))
