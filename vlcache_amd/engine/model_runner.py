@@ -20,6 +20,8 @@ prepare_sample, run_model, run, allocate_kv_cache, exit.  Differences:
     (synthetic_vision), and raises otherwise;
   * every decode plan shares one workspace sized once for max_num_seqs requests
     of up to max_model_len tokens;
+  * with enforce_eager off, decode steps replay HIP graphs captured per batch size
+    on first use (the reference captures CUDA graphs at start-up);
   * no tensor parallelism, no shared-memory RPC: one process, one GPU.
 """
 from __future__ import annotations
