@@ -12,6 +12,7 @@ elements is printed.
 """
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -142,3 +143,38 @@ def test_linear_layer_routes_few_rows_to_the_skinny_kernel(dev):
         assert ((y - ref).abs() <= ref.abs() * 2.0 ** -6 + 2e-3).all(), rows
     y3 = lin(randn_bf16((2, 3, 2048), 7).to(dev))
     assert y3.shape == (2, 3, 512)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes(dev, seed):
+    """Seeded random shapes for the three kernels: RMSNorm (dims multiples of 8 up to
+    8192, 1..3000 rows, with and without the residual), SiLU-and-multiply (inter multiples
+    of 4), and the skinny linear layer (1..16 rows, K multiples of 32, N multiples of 16,
+    with and without bias), each against the oracle / fp32 product to the bars above."""
+    from vlcache_amd import kernels
+
+    rng = np.random.default_rng(100 + seed)
+    rows, dim = int(rng.integers(1, 3000)), 8 * int(rng.integers(1, 1025))
+    say(f"random shapes seed {seed}: rms {rows}x{dim}")
+    x = randn_bf16((rows, dim), seed, float(rng.uniform(0.1, 10)))
+    w = randn_bf16((dim,), seed + 1)
+    if rng.integers(2):
+        r = randn_bf16((rows, dim), seed + 2)
+        out, nr = kernels.rms_norm(x.to(dev), w.to(dev), 1e-6, r.to(dev), residual_out=torch.empty_like(x, device=dev))
+        ref, ref_r = ol.rms_norm(x, w, 1e-6, r)
+        assert torch.equal(nr.cpu().view(torch.int16), ref_r.view(torch.int16))
+    else:
+        out, ref = kernels.rms_norm(x.to(dev), w.to(dev), 1e-6), ol.rms_norm(x, w, 1e-6)
+    _within_ulps(out, ref, f"rms {rows}x{dim}", 2)
+    srows, inter = int(rng.integers(1, 2000)), 4 * int(rng.integers(1, 3000))
+    gu = randn_bf16((srows, 2 * inter), seed + 3, 3.0)
+    _within_ulps(kernels.silu_mul(gu.to(dev)), ol.silu_mul(gu), f"silu {srows}x{inter}")
+    m, k, n = int(rng.integers(1, 17)), 32 * int(rng.integers(1, 400)), 16 * int(rng.integers(1, 2000))
+    xs = randn_bf16((m, k), seed + 4)
+    ws = randn_bf16((n, k), seed + 5, 0.05)
+    b = randn_bf16((n,), seed + 6) if rng.integers(2) else None
+    say(f"skinny {m}x{k}x{n} bias={b is not None}")
+    y = kernels.linear_skinny(xs.to(dev), ws.to(dev), b.to(dev) if b is not None else None).float().cpu()
+    ref = xs.float() @ ws.float().t() + (b.float() if b is not None else 0.0)
+    tol = ref.abs() * 2.0 ** -7 + ref.abs().max() * k * 2.0 ** -24
+    assert int(((y - ref).abs() > tol).sum()) == 0

@@ -268,3 +268,37 @@ def test_engine_runs_the_tower_on_a_cold_image(dev):
     for key, (pv, g) in zip(keys, ((pix2, g2), (pix3, grid))):
         direct = runner.model.visual(pv.to(dev), [g])
         assert torch.equal(cache.get(key).view(torch.int16), direct.view(torch.int16))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_grids(dev, seed):
+    """Seeded random batches of 1-3 images (t 1-2, h and w even, 2..60 patches a side):
+    the window layout equals the oracle's, the rotary kernel is bit-exact, and the
+    80-dim window and whole-image attention pass the per-(row, head) bar."""
+    rng = np.random.default_rng(200 + seed)
+    grids = [(int(rng.integers(1, 3)), 2 * int(rng.integers(1, 31)), 2 * int(rng.integers(1, 31)))
+             for _ in range(int(rng.integers(1, 4)))]
+    say(f"vision random grids seed {seed}: {grids}")
+    lay, qkv, cos, sin = _rope_inputs(dev, grids, seed=300 + seed)
+    idx, cu = ov.window_index(grids, 112, 2, 14)
+    assert np.array_equal(lay.window_index, idx) and lay.cu_window == cu
+    assert lay.cu_full == ov.full_cu_seqlens(grids)
+    heads = kernels.vision_rope_pad(qkv.to(dev), torch.from_numpy(lay.pos_hw).to(dev), cos, sin, 16, 80)
+    hc = heads.cpu()
+    n = lay.num_patches
+    ph, pw = torch.from_numpy(lay.pos_hw[:, 0]).long(), torch.from_numpy(lay.pos_hw[:, 1]).long()
+    c, s = cos.cpu(), sin.cpu()
+    c80 = torch.cat((c[ph], c[pw], c[ph], c[pw]), -1)
+    s80 = torch.cat((s[ph], s[pw], s[ph], s[pw]), -1)
+    q, k, v = qkv.reshape(n, 3, 16, 80).unbind(1)
+    assert torch.equal(hc[:, 0, :, :80].view(torch.int16), ov.rope_bf16(q, c80, s80).view(torch.int16))
+    assert torch.equal(hc[:, 1, :, :80].view(torch.int16), ov.rope_bf16(k, c80, s80).view(torch.int16))
+    assert torch.equal(hc[:, 2, :, :80].view(torch.int16), v.view(torch.int16))
+    for cu_h in (lay.cu_window, lay.cu_full):
+        plan = kernels.plan_attention(cu_h, cu_h, 16, 16, 80, False, dev)
+        cu_t = torch.tensor(cu_h, dtype=torch.int32, device=dev)
+        o = kernels.varlen_attention(heads[:, 0], heads[:, 1], heads[:, 2], cu_t, cu_t, 80 ** -0.5, causal=False,
+                                     plan=plan, head_dim=80).cpu()
+        ref = oattn.varlen_attention(hc[:, 0, :, :80], hc[:, 1, :, :80], hc[:, 2, :, :80], cu_h, cu_h,
+                                     80 ** -0.5, False)
+        assert_attn_close(o[..., :80], ref, what=f"random grids {grids}")
