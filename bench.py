@@ -348,6 +348,61 @@ def run_config(wl_name: str, steps: int, warmup: int, scatter: bool = False):
     return out
 
 
+SWEEP_TOKENS = (256, 1247, 4096, 10741, 32768)
+
+
+def run_bandwidth_sweep(tokens=SWEEP_TOKENS, steps: int = 5):
+    """The two per-layer bandwidth kernels over a range of recomputed-token counts, on
+    Qwen2.5-VL-3B shapes (16/2 heads, head_dim 128, pages of 256), next to a plain
+    device copy that reads and writes the scatter's bytes: where the kernels and the
+    copy both fall short of the large-size rate, the size is launch-bound, not the
+    kernel.  Each figure is per call, 36 calls (one per layer, distinct caches) in one
+    HIP graph, as in the main line."""
+    from vlcache_amd import kernels
+    from vlcache_amd.hotpath import MAX_POSITIONS
+    from vlcache_amd.layers.rotary_embedding import get_rope
+    from vlcache_amd.workloads import BLOCK_SIZE, QWEN25_VL_3B as m, rope_store_bytes, scatter_bytes
+
+    dev = torch.device("cuda:0")
+    hq, hkv, hd, L = m.num_heads, m.num_kv_heads, m.head_dim, m.num_layers
+    rope = get_rope(hd, hd, MAX_POSITIONS, m.rope_theta, {"mrope_section": list(m.mrope_section)}).to(dev)
+    out = {"tokens": list(tokens), "scatter_us": [], "scatter_gbps": [], "rope_store_us": [],
+           "rope_store_gbps": [], "copy_us": [], "copy_gbps": [],
+           "copy": "torch copy_ reading and writing the scatter's bytes (K and V rows)",
+           "timing": "per call: 36 calls (distinct per-layer caches) in one HIP graph, replayed, HIP events"}
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    for n in tokens:
+        nb = -(-n // BLOCK_SIZE)
+        qkv = torch.randn(n, (hq + 2 * hkv) * hd, generator=g, device=dev, dtype=torch.bfloat16)
+        q_in = qkv[:, :hq * hd].view(n, hq, hd)
+        k_in = qkv[:, hq * hd:(hq + hkv) * hd].view(n, hkv, hd)
+        v = qkv[:, (hq + hkv) * hd:].view(n, hkv, hd)
+        k = k_in.contiguous()
+        q = torch.empty(n, hq, hd, device=dev, dtype=torch.bfloat16)
+        kc = torch.zeros(L, nb, BLOCK_SIZE, hkv, hd, device=dev, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        # the engine's layout: a sequence's tokens fill its pages in order, pages in any order
+        pages = torch.randperm(nb, generator=g, device=dev)
+        tok = torch.arange(n, device=dev)
+        slots = (pages[tok // BLOCK_SIZE] * BLOCK_SIZE + tok % BLOCK_SIZE).to(torch.int32)
+        pos = torch.randint(0, 4096, (3, n), generator=g, device=dev, dtype=torch.int64)
+        src = torch.randn(n, 2 * hkv * hd, generator=g, device=dev, dtype=torch.bfloat16)
+        dst = torch.empty(L, n, 2 * hkv * hd, device=dev, dtype=torch.bfloat16)
+        sc = _graph_us_per_call(lambda l: kernels.store_kvcache_raw(k, v, kc[l], vc[l], slots), L, steps)
+        rs = _graph_us_per_call(lambda l: kernels.rope_store_kvcache(pos, q_in, k_in, v, rope.cos_sin_cache,
+                                                                     m.mrope_section, kc[l], vc[l], slots,
+                                                                     q_out=q), L, steps)
+        cp = _graph_us_per_call(lambda l: dst[l].copy_(src), L, steps)
+        sb, rb = scatter_bytes(n, hkv, hd), rope_store_bytes(n, hq, hkv, hd)
+        for key, us, b in (("scatter", sc, sb), ("rope_store", rs, rb), ("copy", cp, sb)):
+            out[f"{key}_us"].append(None if us is None else round(us, 2))
+            out[f"{key}_gbps"].append(None if us is None else round(b / (us * 1e-6) / 1e9, 1))
+        del qkv, q, k, kc, vc, src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_ttft(ratio: float, reps: int = 2):
     """Warm TTFT (ms) of the cold -> warm protocol of the reference's test_partial_recompute.py.
 
@@ -696,6 +751,7 @@ def main():
     ap.add_argument("--no-vision", action="store_true", help="skip the vision tower sub-result")
     ap.add_argument("--no-decode-tail", action="store_true", help="skip the 7B batch's decode tail")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads' sub-results")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the bandwidth kernels' size sweep")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run one plain device-to-device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -724,6 +780,7 @@ def main():
         for name, kw in (("cfg1", {"scatter": True}), ("cfg3", {"scatter": True}), ("cfg4", {}), ("cfg5", {})):
             if name != args.workload:
                 others[name] = run_config(name, args.steps, 1, **kw)
+    sweep = run_bandwidth_sweep() if not args.no_sweep else None
     wl, hp = r["wl"], r["hp"]
     ttft = None
     if not args.no_ttft:
@@ -806,6 +863,7 @@ def main():
         "vision": vision,
         "decode_tail": decode_tail,
         "configs": others,
+        "bandwidth_sweep": sweep,
     }
     print(json.dumps(line), flush=True)
 

@@ -15,6 +15,21 @@ struct alignas(16) u32x4 {
   uint32_t x, y, z, w;
 };
 
+// 16-byte store with the nontemporal cache policy (streamed to HBM rather than kept in
+// L2 and the MALL).  Inline assembly: the compiler folds the nontemporal builtin's
+// store into a plain one where two branches store to different addresses.  The
+// compiler does not count this store in its wait counters; stores never feed a
+// register, and an extra memory operation in flight only makes its vmcnt waits stricter.
+// It does not see the store's hazards either: a VALU write to the data registers of a
+// store of more than 8 bytes needs two wait states after it (gfx940 and later), or the
+// store can send the new values; the compiler reuses those registers at once.  Hence
+// the s_nop 1 inside the statement.
+typedef uint32_t u32x4_vec __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st16_nt(void* p, const u32x4& v) {
+  const u32x4_vec w = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" : : "v"(p), "v"(w) : "memory");
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int launch_status() {

@@ -179,7 +179,10 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
 // loads in its waits, so their results are used only after an explicit vmcnt(0)
 // that takes them as operands.
 __device__ __forceinline__ void st16_agent(void* addr, f32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(addr), "v"(v) : "memory");
+  // s_nop 1: two wait states before a VALU write of the data registers, which the
+  // compiler reuses right after this statement (it does not track the hazard of a
+  // store of more than 8 bytes through inline assembly).
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(addr), "v"(v) : "memory");
 }
 __device__ __forceinline__ f32x4 ld16_agent(const void* addr) {
   f32x4 v;
