@@ -123,22 +123,39 @@ int launch_rms(const void* x, int64_t xs, const void* res, int64_t rs, void* ro,
   return launch_status();
 }
 
+// V = 8: 16-byte accesses (inter % 8 == 0), else 8-byte ones (V = 4).
+template <int V>
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const char* __restrict__ gu, int64_t gu_stride_b,
-                                                            int64_t rows, int quads, int64_t up_offset_b,
+                                                            int64_t rows, int groups, int64_t up_offset_b,
                                                             char* __restrict__ out, int64_t out_stride_b) {
   const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (u >= rows * quads) return;
-  const int64_t row = u / quads;
-  const int q = (int)(u - row * quads);
-  const char* src = gu + row * gu_stride_b + (int64_t)q * 8;
-  const uint2 g = *reinterpret_cast<const uint2*>(src);
-  const uint2 p = *reinterpret_cast<const uint2*>(src + up_offset_b);
-  const float gv[4] = {lo16(g.x), hi16(g.x), lo16(g.y), hi16(g.y)};
-  const float pv[4] = {lo16(p.x), hi16(p.x), lo16(p.y), hi16(p.y)};
-  float y[4];
+  if (u >= rows * groups) return;
+  const int64_t row = u / groups;
+  const int q = (int)(u - row * groups);
+  const char* src = gu + row * gu_stride_b + (int64_t)q * (2 * V);
+  uint32_t g[V / 2], p[V / 2];
+  if constexpr (V == 8) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(src + up_offset_b);
+    g[0] = a.x, g[1] = a.y, g[2] = a.z, g[3] = a.w;
+    p[0] = b.x, p[1] = b.y, p[2] = b.z, p[3] = b.w;
+  } else {
+    const uint2 a = *reinterpret_cast<const uint2*>(src);
+    const uint2 b = *reinterpret_cast<const uint2*>(src + up_offset_b);
+    g[0] = a.x, g[1] = a.y;
+    p[0] = b.x, p[1] = b.y;
+  }
+  uint32_t o[V / 2];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) y[k] = gv[k] / (1.0f + expf(-gv[k])) * pv[k];
-  *reinterpret_cast<uint2*>(out + row * out_stride_b + (int64_t)q * 8) = uint2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+  for (int k = 0; k < V / 2; ++k) {
+    const float g0 = lo16(g[k]), g1 = hi16(g[k]);
+    o[k] = pack2(g0 / (1.0f + expf(-g0)) * lo16(p[k]), g1 / (1.0f + expf(-g1)) * hi16(p[k]));
+  }
+  char* dst = out + row * out_stride_b + (int64_t)q * (2 * V);
+  if constexpr (V == 8)
+    *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+  else
+    *reinterpret_cast<uint2*>(dst) = uint2{o[0], o[1]};
 }
 
 }  // namespace
@@ -189,12 +206,22 @@ VLC_API int vlc_silu_mul(const void* gate_up, int64_t gate_up_row_stride, int64_
   if ((reinterpret_cast<uintptr_t>(gate_up) & 7) || (reinterpret_cast<uintptr_t>(out) & 7) ||
       (gate_up_row_stride % 4) || (out_row_stride % 4))
     return VLC_ERR_UNSUPPORTED;
-  const int quads = (int)(inter / 4);
-  const int64_t total = num_rows * quads;
+  // 16-byte accesses when the call is large enough to fill the device with half as
+  // many lanes: 1247 x 11008 in 17.2 against 18.9 us, 10741 x 11008 in 125 against
+  // 139 us; a decode step's 4 x 18944 measured 2.2 against 2.05 us with them.
+  const bool v16 = inter % 8 == 0 && num_rows * inter >= ((int64_t)1 << 20) && aligned16(gate_up) &&
+                   aligned16(out) && gate_up_row_stride % 8 == 0 && out_row_stride % 8 == 0;
+  const int groups = (int)(inter / (v16 ? 8 : 4));
+  const int64_t total = num_rows * groups;
   const int64_t blocks = (total + kThreads - 1) / kThreads;
   if (blocks >= ((int64_t)1 << 31)) return VLC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream),
-                     static_cast<const char*>(gate_up), gate_up_row_stride * 2, num_rows, quads, inter * 2,
-                     static_cast<char*>(out), out_row_stride * 2);
+  if (v16)
+    hipLaunchKernelGGL(silu_mul_kernel<8>, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream),
+                       static_cast<const char*>(gate_up), gate_up_row_stride * 2, num_rows, groups, inter * 2,
+                       static_cast<char*>(out), out_row_stride * 2);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<4>, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream),
+                       static_cast<const char*>(gate_up), gate_up_row_stride * 2, num_rows, groups, inter * 2,
+                       static_cast<char*>(out), out_row_stride * 2);
   return launch_status();
 }
