@@ -97,6 +97,13 @@ def test_scatter_random_shapes(dev, seed):
     _scatter_case(dev, n, hkv, hd, nb, bs, seed=500 + seed, dtype=dtype, neg_every=neg, v_row=v_row)
 
 
+def test_scatter_call_above_the_nontemporal_limit(dev):
+    """A scatter that writes more than 256 MB (65600 tokens x 8 kv heads x 128 dims, K and V:
+    269 MB) takes the plain-store kernel; bit for bit, with skipped slots."""
+    say("scatter: 65600 tokens x 8 x 128 (269 MB written, plain stores), slot -1 every 13th")
+    _scatter_case(dev, 65600, 8, 128, 258, 256, seed=77, neg_every=13)
+
+
 # ----------------------------------------------------------------------------- rerotate
 def _rerotate_setup(L, nb, seed, hkv=2, hd=128):
     g = gen(seed)
@@ -289,6 +296,14 @@ def test_rope_store_random_shapes(dev, seed):
     kw = dict(in_place=bool(r.random() < 0.5), want_k=bool(r.random() < 0.5), neg_every=int(r.choice([0, 5])))
     say(f"rope_store random seed={seed}: n={n} heads={hq}/{hkv} section={section} {kw}")
     _rope_case(dev, pos, hq, hkv, section, seed=600 + seed, nb=nb, **kw)
+
+
+def test_rope_store_call_above_the_nontemporal_limit(dev):
+    """A fused RoPE + store call that writes more than 256 MB (53000 tokens of 16/2 heads: q_out
+    and the cache's k and v, 271 MB) takes the plain-store kernel; bit for bit, M-RoPE."""
+    say("rope_store: 53000 tokens, 16/2 heads, M-RoPE [16,24,24] (271 MB written, plain stores)")
+    pos = np.random.default_rng(46).integers(0, 16000, (3, 53000))
+    _rope_case(dev, pos, 16, 2, [16, 24, 24], seed=46, nb=-(-53000 // 256) + 1, neg_every=0)
 
 
 def test_rope_store_4k_image_recomputed_mrope(dev):

@@ -27,11 +27,11 @@
 // accesses.  Each lane handles kUPT units spaced by the grid, all their loads
 // in flight before the first store; one unit per lane (the most workgroups)
 // measured fastest for the 1247-token warm step (4.5 us against 5.1 us with two).
-// Every store is nontemporal (streamed to HBM): 1247 / 10741 / 32768 tokens in
-// 3.7-3.9 / 19.5 / 54.0 us against 4.1 / 20.4 / 60 us with plain stores (36 calls
-// in one graph, distinct caches), and the attention that reads q_out next timed
-// the same; nontemporal cache stores with a plain q_out store gained less (4.1 /
-// 19.9 / 59 us).
+// Every store is nontemporal (streamed to HBM) when the call writes at most
+// kNtMaxWriteBytes: 1247 / 10741 / 32768 tokens in 3.7-3.9 / 19.5 / 54.0 us against
+// 4.1 / 20.4 / 60 us with plain stores (36 calls in one graph, distinct caches), and
+// the attention that reads q_out next timed the same; nontemporal cache stores with a
+// plain q_out store gained less (4.1 / 19.9 / 59 us).
 #include "common.h"
 
 namespace vlc {
@@ -93,7 +93,7 @@ __device__ __forceinline__ int64_t clamp_pos(int64_t p, int64_t max_pos) {
 // bounds are multiples of 8) and cos/sin rows are 16-byte aligned, so a unit
 // reads one position and 2 x 32 contiguous bytes of cos/sin.  kPerPair = true:
 // position and cos/sin are read pair by pair (any section bounds, any alignment).
-template <bool kPerPair>
+template <bool kPerPair, bool kNt>
 __global__ __launch_bounds__(kThreads) void rope_store_kv_kernel(const RopeArgs a) {
   const int hd = a.head_dim;
   const int half = hd >> 1;
@@ -202,13 +202,13 @@ __global__ __launch_bounds__(kThreads) void rope_store_kv_kernel(const RopeArgs 
                      : (x.kind == 1 ? a.k_cache : a.v_cache) + (int64_t)x.slot * row_elems;
       const bool st0 = x.live && (x.kind == 0 || (store && slot_ok));
       if (st0) {
-        st16_nt(dst0 + x.off, lo);
-        st16_nt(dst0 + x.off + half, hi);
+        st16<kNt>(dst0 + x.off, lo);
+        st16<kNt>(dst0 + x.off + half, hi);
       }
       if (x.live && x.kind == 1 && a.k_out) {
         uint16_t* dst1 = a.k_out + (int64_t)x.n * a.ko_rs + x.off;
-        st16_nt(dst1, lo);
-        st16_nt(dst1 + half, hi);
+        st16<kNt>(dst1, lo);
+        st16<kNt>(dst1 + half, hi);
       }
     }
   }
@@ -297,9 +297,12 @@ VLC_API int vlc_rope_store_kvcache(const void* q, int64_t q_row_stride, void* q_
   const bool per_pair = !aligned16(cos_sin_cache) || cache_row_stride % 4 != 0 || b1 % 8 != 0 || b2 % 8 != 0;
   int64_t blocks = (total + (int64_t)kThreads * kUPT - 1) / ((int64_t)kThreads * kUPT);
   if (blocks > 65535) blocks = 65535;
-  if (per_pair)
-    hipLaunchKernelGGL(rope_store_kv_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), a);
-  else
-    hipLaunchKernelGGL(rope_store_kv_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), a);
+  // bytes written: q_out, the cache's k and v rows, k_out
+  const int64_t written = num_tokens * head_dim * 2 *
+                          ((int64_t)num_heads_q + (store ? 2 : 0) * num_heads_kv + (k_out ? num_heads_kv : 0));
+  const bool nt = written <= kNtMaxWriteBytes;
+  auto kernel = per_pair ? (nt ? rope_store_kv_kernel<true, true> : rope_store_kv_kernel<true, false>)
+                         : (nt ? rope_store_kv_kernel<false, true> : rope_store_kv_kernel<false, false>);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), a);
   return launch_status();
 }
