@@ -461,11 +461,16 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     // stays before it (the compiler would otherwise sink the softmax past the
     // barrier at the end of the step, next to its consumers).
     auto pin = [](float& x) __attribute__((always_inline)) { asm volatile("" : "+v"(x)); };
+    // The row sum adds each exp2 result one exp later (pend holds the last one): an
+    // add right behind its transcendental needs a wait state, which the compiler
+    // fills with an s_nop.
+    float pend = 0.f;
     auto exp_elem = [&](int n) __attribute__((always_inline)) {
       float pe = fast_exp2(__builtin_fmaf(get(n), p.scale_log2, -m_base));
       pin(pe);
       set(n, pe);
-      rs += pe;
+      if (n > 0) rs += pend;
+      pend = pe;
     };
 
     // exp2 slices: units 4 .. 4 + kTwo - 1 take two elements each, the rest one, so the
@@ -521,6 +526,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    rs += pend;
     l_run = l_run * alpha + rs;
     // P^T as bf16 B operands: chunk ch of key block kb = elements 8ch .. 8ch+7
 #pragma unroll
