@@ -620,7 +620,9 @@ def run_vision(reps: int = 5):
     kernels of a block's attention on the same layout, each the median of 20
     event-timed calls: the fused rotary + head padding (HBM: bytes read + written),
     the window attention and the whole-image attention (MFMA: 4 * pairs * 80 dims
-    * 16 heads; the kernel's 80-dim variant skips the heads' zero padding).
+    * 16 heads; the kernel's 80-dim variant skips the heads' zero padding; HBM: the q, k, v
+    head rows read once and the output written once, which bounds the window attention's
+    64-token windows).
     """
     from vlcache_amd import kernels
     from vlcache_amd.config import QWEN25_VL_VISION
@@ -686,9 +688,13 @@ def run_vision(reps: int = 5):
         ms = med_ms(attn(cu, plan))
         pairs = sum((b - a) ** 2 for a, b in zip(cu_host, cu_host[1:]))
         tf = 4.0 * pairs * hd * h / (ms * 1e-3) / 1e12
+        # bytes the kernel moves at least: q, k and v head rows read (128-element rows), output written
+        nbytes = 4 * n * h * kernels.HEAD_DIM * 2
         out[name] = {"ms": round(ms, 4), "sequences": len(cu_host) - 1, "work_items": plan.num_items,
                      "kernel_head_dim": run.attn_head_dim, "tflops": round(tf, 1),
-                     "frac_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+                     "frac_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
     del vt, heads, o, qkv
     torch.cuda.empty_cache()
     return out
