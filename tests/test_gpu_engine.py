@@ -385,3 +385,47 @@ def test_decode_graph_replays_match_the_eager_decode(dev):
         eng.scheduler.postprocess(seqs, le.argmax(-1).tolist())
     assert seen == {1, 2, 3}, seen
     assert set(runner._graphs) == {1, 2, 4}
+
+
+def test_partial_warm_ttft_below_nine_tenths_of_full_recompute(dev):
+    """The reference's pass rule (test_partial_recompute.py:151-152): the warm request's TTFT with
+    recompute_ratio=0.1 is below 0.9 x its TTFT with recompute_ratio=0.0 (full recompute).
+
+    Protocol of test_partial_recompute.py:65-89 on a random-init model with Qwen2.5-VL-3B text
+    shapes cut to 6 layers (vocab 1000): per engine, a cold request (prefix 40, suffix 64) caches
+    the image, then a warm request (prefix 128, suffix 64) reuses it.  The image is a (1, 128, 128)
+    grid: 4096 image tokens, so prefill work, not host overhead, sets the full-recompute TTFT.
+    The first image of each engine warms up kernels and libraries; the medians of two further
+    images are compared."""
+    from vlcache_amd import LLM
+    from vlcache_amd.config import QWEN25_VL_3B
+
+    say("engine: warm TTFT, ratio 0.1 vs ratio 0.0 (reference pass rule: < 0.9x)")
+    cfg = {k: v for k, v in QWEN25_VL_3B.items() if k != "vision_config"}
+    cfg.update(num_hidden_layers=6, vocab_size=1000, image_token_id=IMG, eos_token_id=0,
+               max_position_embeddings=8192)
+    grid = (1, 128, 128)
+    sp = SamplingParams(temperature=0.6, max_tokens=1)
+
+    def warm_ttft(ratio):
+        llm = LLM(dict(cfg), recompute_ratio=ratio, num_kvcache_blocks=160, max_model_len=8192,
+                  max_num_batched_tokens=8192, synthetic_vision=True, enforce_eager=True)
+        warm = []
+        for r in range(3):
+            toks_a, mm = _request(40, grid, 64, seed=10 + r)
+            mm = {"pixel_values": mm["pixel_values"] + r, "image_grid_thw": mm["image_grid_thw"]}
+            toks_b, _ = _request(128, grid, 64, seed=20 + r)
+            o1 = llm.generate([toks_a], sp, mm_inputs=[mm])
+            o2 = llm.generate([toks_b], sp, mm_inputs=[mm])
+            assert o2[0]["vit_time"] == 0.0  # encoder-cache hit
+            if r > 0:
+                warm.append(o2[0]["ttft"])
+        del llm
+        torch.cuda.empty_cache()
+        return float(np.median(warm))
+
+    full = warm_ttft(0.0)
+    part = warm_ttft(0.1)
+    say(f"warm TTFT: full recompute {full * 1e3:.2f} ms, partial 0.1 {part * 1e3:.2f} ms "
+        f"({full / part:.2f}x)")
+    assert part < 0.9 * full
