@@ -649,10 +649,73 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 // with Ohat_s = O_s / l_s stored in bf16.  grid = (combine items, kCols /
 // kCombineCols): a workgroup owns kCombineCols columns and each lane one 8-dim
 // (16-byte) slice of a column.  The merge is latency-bound (a few KB per split),
-// so both passes keep many loads in flight: the 16 lanes of a column share the
-// (m, l) loads of the max and reduce it with shuffles, and the weighted sum is
-// unrolled 16 splits deep.
+// so it keeps many loads in flight: the 16 lanes of a column share the (m, l)
+// loads of the max and reduce it with shuffles, and the weighted sum is unrolled
+// B splits deep.  The first B partials do not depend on the max, so they are
+// loaded together with the maxima: one round trip instead of two.
 constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 16 columns per workgroup
+
+// Weighted sum of one column slice over the splits: acc = sum_s w_s Ohat_s and the
+// return value sum_s w_s, w_s = 2^(m_s - M) l_s.  Loads are batched explicitly
+// (indices clamped to the last split, extra terms weighted 0) so that a batch is in
+// flight at once.
+template <int B>
+__device__ __forceinline__ float combine_slice(const float* ml, const uint16_t* po, int nsplit, int sub,
+                                              float (&acc)[8]) {
+  constexpr int kLanes = kHeadDim / 8;  // lanes per column
+  constexpr int64_t ml_stride = (int64_t)kCols * 2;
+  constexpr int64_t po_stride = (int64_t)kCols * kHeadDim;
+  float m4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) m4[k] = ml[min(sub + k * kLanes, nsplit - 1) * ml_stride];
+  auto load_batch = [&](int s0, float2(&mls)[B], u32x4v(&v)[B]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const int s = min(s0 + k, nsplit - 1);
+      mls[k] = *reinterpret_cast<const float2*>(ml + s * ml_stride);
+      v[k] = *reinterpret_cast<const u32x4v*>(po + s * po_stride);
+    }
+  };
+  float2 mls0[B];
+  u32x4v v0[B];
+  load_batch(0, mls0, v0);
+  float mmax = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k]);
+  for (int s0 = 4 * kLanes; s0 < nsplit; s0 += 4 * kLanes) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m4[k] = ml[min(s0 + sub + k * kLanes, nsplit - 1) * ml_stride];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k]);
+  }
+#pragma unroll
+  for (int x = 1; x < kLanes; x <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, x));
+  // Every split empty (mmax = -inf): every weight is 0.  The first batch is used
+  // unconditionally, so the compiler cannot sink its loads below the max.
+  const bool any = mmax != -INFINITY;
+  float lsum = 0.f;
+  auto accumulate = [&](int s0, const float2(&mls)[B], const u32x4v(&v)[B]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const float wl = any && s0 + k < nsplit ? fast_exp2(mls[k].x - mmax) * mls[k].y : 0.f;
+      lsum += wl;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
+        acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
+      }
+    }
+  };
+  accumulate(0, mls0, v0);
+  // Later batches in arrays of their own: no batch stays live across iterations.
+  for (int s0 = B; s0 < nsplit; s0 += B) {
+    float2 mls[B];
+    u32x4v v[B];
+    load_batch(s0, mls, v);
+    accumulate(s0, mls, v);
+  }
+  return lsum;
+}
 
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) {
   const int32_t* it = p.combine + (int64_t)blockIdx.x * kItemInts;
@@ -663,59 +726,16 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) 
   const int col = blockIdx.y * kCombineCols + threadIdx.x / (kHeadDim / 8);
   const int d = 8 * sub;
   const int pos = col / p.group;
-  const bool valid = pos < q_count;  // whole 16-lane groups agree (same column)
+  // Whole 16-lane groups agree (same column), so the shuffles inside stay within
+  // active lanes.
+  if (pos >= q_count) return;
   const float* ml = p.part_ml + ((int64_t)first * kCols + col) * 2;
   const uint16_t* po = p.part_o + ((int64_t)first * kCols + col) * kHeadDim + d;
-  const int64_t ml_stride = (int64_t)kCols * 2;
-  const int64_t po_stride = (int64_t)kCols * kHeadDim;
-  // Loads are batched explicitly (indices clamped to the last split, extra terms
-  // weighted 0) so that a batch is in flight at once.
-  constexpr int kLanes = kHeadDim / 8;  // lanes per column
-  constexpr int kBatch = 16;
-  float mmax = -INFINITY;
-  if (valid) {
-    for (int s0 = 0; s0 < nsplit; s0 += 4 * kLanes) {
-      float m4[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) m4[k] = ml[min(s0 + sub + k * kLanes, nsplit - 1) * ml_stride];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k]);
-    }
-  }
-#pragma unroll
-  for (int x = 1; x < kLanes; x <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, x));
-  if (!valid) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  auto merge = [&](auto batch) __attribute__((always_inline)) {
-    constexpr int B = decltype(batch)::value;
-    for (int s0 = 0; s0 < nsplit; s0 += B) {
-      float2 mls[B];
-      u32x4v v[B];
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        const int s = min(s0 + k, nsplit - 1);
-        mls[k] = *reinterpret_cast<const float2*>(ml + s * ml_stride);
-        v[k] = *reinterpret_cast<const u32x4v*>(po + s * po_stride);
-      }
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        const float wl = s0 + k < nsplit ? fast_exp2(mls[k].x - mmax) * mls[k].y : 0.f;
-        lsum += wl;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
-          acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
-        }
-      }
-    }
-  };
-  if (mmax != -INFINITY) {
-    // Batch depth by split count: deep batches for long merges, no wasted loads
-    // for short ones.
-    if (nsplit > 8) merge(std::integral_constant<int, kBatch>{});
-    else merge(std::integral_constant<int, 4>{});
-  }
+  // Batch depth by split count: deep batches for long merges, no wasted loads for
+  // short ones.
+  const float lsum = nsplit > 8 ? combine_slice<16>(ml, po, nsplit, sub, acc)
+                                : combine_slice<4>(ml, po, nsplit, sub, acc);
   const int hh = col - pos * p.group;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
