@@ -30,6 +30,22 @@ __device__ __forceinline__ void st16_nt(void* p, const u32x4& v) {
   asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" : : "v"(p), "v"(w) : "memory");
 }
 
+// 16-byte store at agent scope (sc1): written through the XCD's L2 to the memory side,
+// so it leaves no dirty line in L2.  Each kernel ends with a write-back of its XCDs'
+// dirty L2 lines before the next kernel on the stream starts; a kernel whose output the
+// next kernel reads spends that time after its last workgroup.  Measured on the warm
+// attention call (main kernel, then the split-KV merge): the gap between the two
+// kernels fell from 2.6 to 1.2 us with these stores for the outputs and partials
+// (nontemporal stores, which still leave the lines dirty, changed nothing).  Same
+// inline-assembly caveats as st16_nt.
+__device__ __forceinline__ void st16_wt(void* p, const u32x4_vec& w) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(w) : "memory");
+}
+// 8-byte store at agent scope: the compiler's relaxed atomic store (it tracks its hazards).
+__device__ __forceinline__ void st8_wt(void* p, uint64_t bits) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // 16-byte store, nontemporal when kNt.
 template <bool kNt>
 __device__ __forceinline__ void st16(void* p, const u32x4& v) {

@@ -607,7 +607,9 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   // chunk c of column x at slot c ^ (x & 15)) and then stored as whole rows, 16
   // bytes per lane: the rows of the `group` heads of one position are adjacent in
   // the output (and all rows of a workspace slot are), so each store instruction
-  // writes 1 KB of contiguous memory.  The K buffers are free here.
+  // writes 1 KB of contiguous memory.  The stores write through L2 (st16_wt): the
+  // next kernel reads them, and dirty L2 lines would be written back between the two
+  // kernels.  The K buffers are free here.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   uint8_t* stage = (wave < 2 ? k_buf0 : k_buf1) + (wave & 1) * (kTileK * 256 / 2);
@@ -634,14 +636,12 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
       uint16_t* dst = slot < 0 ? p.out + (int64_t)(q0 + q_start + posx) * p.out_row_stride +
                                      (int64_t)(g * p.group + colx - posx * p.group) * kHeadDim
                                : p.part_o + ((int64_t)slot * kCols + colx) * kHeadDim;
-      *reinterpret_cast<u32x4v*>(dst + 8 * ch) = v;
+      st16_wt(dst + 8 * ch, v);
     }
   }
-  if (slot >= 0 && valid && hf == 0) {
-    float* ml = p.part_ml + ((int64_t)slot * kCols + col) * 2;
-    ml[0] = m_run;
-    ml[1] = l_tot;
-  }
+  if (slot >= 0 && valid && hf == 0)
+    st8_wt(p.part_ml + ((int64_t)slot * kCols + col) * 2,
+           (uint64_t)__float_as_uint(m_run) | ((uint64_t)__float_as_uint(l_tot) << 32));
 }
 
 // Merge the split-KV partials of one query tile:
@@ -743,7 +743,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) 
   u32x4v w;
 #pragma unroll
   for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
-  *reinterpret_cast<u32x4v*>(orow) = w;
+  st16_wt(orow, w);
 }
 
 }  // namespace
