@@ -28,6 +28,7 @@
 // key range was split write their normalised O (bf16) with (m, l) to a
 // workspace slot; attn_combine merges the slots of a query tile.
 #include <type_traits>
+#include <utility>
 
 #include "attn_plan.h"
 #include "common.h"
@@ -656,65 +657,110 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 16 columns per workgroup
 
 // Weighted sum of one column slice over the splits: acc = sum_s w_s Ohat_s and the
-// return value sum_s w_s, w_s = 2^(m_s - M) l_s.  Loads are batched explicitly
-// (indices clamped to the last split, extra terms weighted 0) so that a batch is in
-// flight at once.
-template <int B>
-__device__ __forceinline__ float combine_slice(const float* ml, const uint16_t* po, int nsplit, int sub,
-                                              float (&acc)[8]) {
-  constexpr int kLanes = kHeadDim / 8;  // lanes per column
-  constexpr int64_t ml_stride = (int64_t)kCols * 2;
-  constexpr int64_t po_stride = (int64_t)kCols * kHeadDim;
-  float m4[4];
+// return value sum_s w_s, w_s = 2^(m_s - M) l_s.  The 16 lanes of a column form one
+// DPP row: lane j loads (m, l) of splits j, j + 16, j + 32, j + 48 of each chunk of 64,
+// computes their weights, and a row broadcast (row_newbcast) hands w_s to the row when
+// split s is accumulated, so (m, l) is loaded once per split and column instead of
+// once per lane.  The partials are loaded in batches of B (indices clamped to the last
+// split, extra terms weighted 0) so that a batch is in flight at once; the first batch
+// does not depend on the max and is issued with the (m, l) loads.
+constexpr int kCombineLanes = kHeadDim / 8;  // lanes per column = one DPP row
+static_assert(kCombineLanes == 16, "a column is one DPP row");
+constexpr int64_t kPartMlStride = (int64_t)kCols * 2;
+constexpr int64_t kPartOStride = (int64_t)kCols * kHeadDim;
+
+template <int J>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + J, 0xf,
+                                                               0xf, false));
+}
+
+struct CombineAcc {
+  float acc[8];
+  float lsum;
+};
+
+// Splits s16 + J0 + k, k < B, whose weights lanes J0 + k of the row hold in wsrc.
+template <int J0, int B, int... K>
+__device__ __forceinline__ void accumulate_batch(std::integer_sequence<int, K...>, float wsrc,
+                                                 const u32x4v (&v)[B], CombineAcc& a) {
+  auto one = [&](auto j, const u32x4v& x) __attribute__((always_inline)) {
+    const float wl = row_bcast<decltype(j)::value>(wsrc);
+    a.lsum += wl;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) m4[k] = ml[min(sub + k * kLanes, nsplit - 1) * ml_stride];
-  auto load_batch = [&](int s0, float2(&mls)[B], u32x4v(&v)[B]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < B; ++k) {
-      const int s = min(s0 + k, nsplit - 1);
-      mls[k] = *reinterpret_cast<const float2*>(ml + s * ml_stride);
-      v[k] = *reinterpret_cast<const u32x4v*>(po + s * po_stride);
+    for (int t = 0; t < 4; ++t) {
+      a.acc[2 * t] += wl * bf16_bits_to_f32(x[t] & 0xffffu);
+      a.acc[2 * t + 1] += wl * bf16_bits_to_f32(x[t] >> 16);
     }
   };
-  float2 mls0[B];
+  (one(std::integral_constant<int, J0 + K>{}, v[K]), ...);
+}
+
+template <int B>
+__device__ __forceinline__ void load_partials(const uint16_t* po, int s0, int nsplit, u32x4v (&v)[B]) {
+#pragma unroll
+  for (int k = 0; k < B; ++k) v[k] = *reinterpret_cast<const u32x4v*>(po + min(s0 + k, nsplit - 1) * kPartOStride);
+}
+
+// The batches of one broadcast slot (splits s16 .. s16 + 15) from J0 on, stopping at nsplit.
+template <int J0, int B>
+__device__ __forceinline__ void slot_batches(const uint16_t* po, int s16, int nsplit, float wsrc, CombineAcc& a) {
+  if constexpr (J0 < kCombineLanes) {
+    if (s16 + J0 >= nsplit) return;
+    u32x4v v[B];
+    load_partials<B>(po, s16 + J0, nsplit, v);
+    accumulate_batch<J0, B>(std::make_integer_sequence<int, B>{}, wsrc, v, a);
+    slot_batches<J0 + B, B>(po, s16, nsplit, wsrc, a);
+  }
+}
+
+template <int B>
+__device__ __forceinline__ void combine_slice(const float* ml, const uint16_t* po, int nsplit, int sub,
+                                              CombineAcc& a) {
+  static_assert(kCombineLanes % B == 0, "a batch lies inside one broadcast slot");
+  constexpr int kChunk = 4 * kCombineLanes;  // splits whose (m, l) one load round covers
+  auto load_ml = [&](int c0, float2(&m4)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      m4[k] = *reinterpret_cast<const float2*>(ml + min(c0 + sub + k * kCombineLanes, nsplit - 1) * kPartMlStride);
+  };
+  float2 m4[4];
+  load_ml(0, m4);
   u32x4v v0[B];
-  load_batch(0, mls0, v0);
+  load_partials<B>(po, 0, nsplit, v0);
   float mmax = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k]);
-  for (int s0 = 4 * kLanes; s0 < nsplit; s0 += 4 * kLanes) {
+  for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k].x);
+  for (int c0 = kChunk; c0 < nsplit; c0 += kChunk) {
+    float2 mc[4];
+    load_ml(c0, mc);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) m4[k] = ml[min(s0 + sub + k * kLanes, nsplit - 1) * ml_stride];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, m4[k]);
+    for (int k = 0; k < 4; ++k) mmax = fmaxf(mmax, mc[k].x);
   }
 #pragma unroll
-  for (int x = 1; x < kLanes; x <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, x));
+  for (int x = 1; x < kCombineLanes; x <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, x));
   // Every split empty (mmax = -inf): every weight is 0.  The first batch is used
   // unconditionally, so the compiler cannot sink its loads below the max.
   const bool any = mmax != -INFINITY;
-  float lsum = 0.f;
-  auto accumulate = [&](int s0, const float2(&mls)[B], const u32x4v(&v)[B]) __attribute__((always_inline)) {
+  float w4[4];
+  auto weights = [&](int c0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int k = 0; k < B; ++k) {
-      const float wl = any && s0 + k < nsplit ? fast_exp2(mls[k].x - mmax) * mls[k].y : 0.f;
-      lsum += wl;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[2 * t] += wl * bf16_bits_to_f32(v[k][t] & 0xffffu);
-        acc[2 * t + 1] += wl * bf16_bits_to_f32(v[k][t] >> 16);
-      }
-    }
+    for (int k = 0; k < 4; ++k)
+      w4[k] = any && c0 + sub + k * kCombineLanes < nsplit ? fast_exp2(m4[k].x - mmax) * m4[k].y : 0.f;
   };
-  accumulate(0, mls0, v0);
-  // Later batches in arrays of their own: no batch stays live across iterations.
-  for (int s0 = B; s0 < nsplit; s0 += B) {
-    float2 mls[B];
-    u32x4v v[B];
-    load_batch(s0, mls, v);
-    accumulate(s0, mls, v);
+  weights(0);
+  accumulate_batch<0, B>(std::make_integer_sequence<int, B>{}, w4[0], v0, a);
+  slot_batches<B, B>(po, 0, nsplit, w4[0], a);
+  for (int s16 = kCombineLanes; s16 < nsplit; s16 += kCombineLanes) {
+    const int c0 = s16 & ~(kChunk - 1);
+    if (c0 == s16) {
+      load_ml(c0, m4);
+      weights(c0);
+    }
+    const int slot = (s16 - c0) / kCombineLanes;
+    const float wsrc = slot == 0 ? w4[0] : slot == 1 ? w4[1] : slot == 2 ? w4[2] : w4[3];
+    slot_batches<0, B>(po, s16, nsplit, wsrc, a);
   }
-  return lsum;
 }
 
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) {
@@ -731,11 +777,15 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const Params p) 
   if (pos >= q_count) return;
   const float* ml = p.part_ml + ((int64_t)first * kCols + col) * 2;
   const uint16_t* po = p.part_o + ((int64_t)first * kCols + col) * kHeadDim + d;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  CombineAcc a = {};
   // Batch depth by split count: deep batches for long merges, no wasted loads for
   // short ones.
-  const float lsum = nsplit > 8 ? combine_slice<16>(ml, po, nsplit, sub, acc)
-                                : combine_slice<4>(ml, po, nsplit, sub, acc);
+  if (nsplit > 8)
+    combine_slice<16>(ml, po, nsplit, sub, a);
+  else
+    combine_slice<4>(ml, po, nsplit, sub, a);
+  const float lsum = a.lsum;
+  const float(&acc)[8] = a.acc;
   const int hh = col - pos * p.group;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   uint16_t* orow = p.out + (int64_t)(q0 + q_start + pos) * p.out_row_stride +
