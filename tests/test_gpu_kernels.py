@@ -104,6 +104,13 @@ def test_scatter_call_above_the_nontemporal_limit(dev):
     _scatter_case(dev, 65600, 8, 128, 258, 256, seed=77, neg_every=13)
 
 
+def test_scatter_call_between_the_store_limits(dev):
+    """A scatter that writes between 64 and 256 MB (24000 tokens x 8 kv heads x 128 dims: 98 MB)
+    takes the nontemporal-store kernel (smaller calls store at agent scope); bit for bit."""
+    say("scatter: 24000 tokens x 8 x 128 (98 MB written, nontemporal stores), slot -1 every 11th")
+    _scatter_case(dev, 24000, 8, 128, 95, 256, seed=78, neg_every=11)
+
+
 # ----------------------------------------------------------------------------- rerotate
 def _rerotate_setup(L, nb, seed, hkv=2, hd=128):
     g = gen(seed)
@@ -304,6 +311,14 @@ def test_rope_store_call_above_the_nontemporal_limit(dev):
     say("rope_store: 53000 tokens, 16/2 heads, M-RoPE [16,24,24] (271 MB written, plain stores)")
     pos = np.random.default_rng(46).integers(0, 16000, (3, 53000))
     _rope_case(dev, pos, 16, 2, [16, 24, 24], seed=46, nb=-(-53000 // 256) + 1, neg_every=0)
+
+
+def test_rope_store_call_between_the_store_limits(dev):
+    """A fused RoPE + store call that writes between 64 and 256 MB (20000 tokens of 16/2 heads:
+    102 MB) takes the nontemporal-store kernel (smaller calls store at agent scope); bit for bit."""
+    say("rope_store: 20000 tokens, 16/2 heads, M-RoPE [16,24,24] (102 MB written, nontemporal stores)")
+    pos = np.random.default_rng(47).integers(0, 16000, (3, 20000))
+    _rope_case(dev, pos, 16, 2, [16, 24, 24], seed=47, nb=-(-20000 // 256) + 1, neg_every=0)
 
 
 def test_rope_store_4k_image_recomputed_mrope(dev):

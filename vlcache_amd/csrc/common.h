@@ -46,20 +46,35 @@ __device__ __forceinline__ void st8_wt(void* p, uint64_t bits) {
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 16-byte store, nontemporal when kNt.
-template <bool kNt>
+// Store policies of the bandwidth kernels' 16-byte stores.
+enum StoreMode : int { kStPlain = 0, kStNt = 1, kStWt = 2 };
+
+template <int kMode>
 __device__ __forceinline__ void st16(void* p, const u32x4& v) {
-  if constexpr (kNt)
+  if constexpr (kMode == kStNt) {
     st16_nt(p, v);
-  else
+  } else if constexpr (kMode == kStWt) {
+    const u32x4_vec w = {v.x, v.y, v.z, v.w};
+    st16_wt(p, w);
+  } else {
     *reinterpret_cast<u32x4*>(p) = v;
+  }
 }
 
-// Calls that write at most this many bytes store nontemporally.  Measured: the scatter and
-// the fused RoPE + store ran faster with nontemporal stores for calls writing 1-170 MB
-// (e.g. 22 MB of scatter in 3.16 against 4.29 us), while larger writes ran slower with them
-// (the 350 MB of K and V written by the re-rotation, the 594 MB of vision head rows).
+// Store policy by the bytes a call writes.  Agent-scope stores (no dirty L2 lines left
+// for the write-back at the kernel's end) up to kWtMaxWriteBytes: the warm request's
+// step (re-rotation, then per layer the fused RoPE + store and the attention) as one
+// graph took 1.231 against 1.249 ms with them in the fused RoPE + store, and the scatter
+// measured 0-7 % faster at 0.5-34 MB; at 168 MB the fused RoPE + store ran 9 % slower
+// with them.  Nontemporal stores up to kNtMaxWriteBytes: they ran faster than plain
+// ones for calls writing 1-170 MB (e.g. 22 MB of scatter in 3.16 against 4.29 us) and
+// slower for larger writes (the 350 MB of K and V written by the re-rotation, the
+// 594 MB of vision head rows).  Plain stores above.
+constexpr int64_t kWtMaxWriteBytes = (int64_t)64 << 20;
 constexpr int64_t kNtMaxWriteBytes = (int64_t)256 << 20;
+inline int store_mode_for(int64_t written_bytes) {
+  return written_bytes <= kWtMaxWriteBytes ? kStWt : written_bytes <= kNtMaxWriteBytes ? kStNt : kStPlain;
+}
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -27,11 +27,17 @@
 // accesses.  Each lane handles kUPT units spaced by the grid, all their loads
 // in flight before the first store; one unit per lane (the most workgroups)
 // measured fastest for the 1247-token warm step (4.5 us against 5.1 us with two).
-// Every store is nontemporal (streamed to HBM) when the call writes at most
-// kNtMaxWriteBytes: 1247 / 10741 / 32768 tokens in 3.7-3.9 / 19.5 / 54.0 us against
-// 4.1 / 20.4 / 60 us with plain stores (36 calls in one graph, distinct caches), and
-// the attention that reads q_out next timed the same; nontemporal cache stores with a
-// plain q_out store gained less (4.1 / 19.9 / 59 us).
+// The stores take the policy store_mode_for picks from the bytes the call writes: at
+// agent scope (written through L2, so the attention that reads q_out and the cache
+// next starts without waiting for a write-back of dirty lines) up to 64 MB,
+// nontemporal up to 256 MB, plain above.  Nontemporal against plain: 1247 / 10741 /
+// 32768 tokens in 3.7-3.9 / 19.5 / 54.0 us against 4.1 / 20.4 / 60 us (36 calls in one
+// graph, distinct caches); nontemporal cache stores with a plain q_out store gained
+// less (4.1 / 19.9 / 59 us).  Agent scope against nontemporal in the same loop: 3.76
+// against 3.67 us at 1247 tokens, 6.45 against 6.71 at 4096, 59.9 against 54.9 at 32768;
+// in the warm request's step, where the attention follows, 1.231 against 1.249 ms.
+#include <type_traits>
+
 #include "common.h"
 
 namespace vlc {
@@ -93,7 +99,7 @@ __device__ __forceinline__ int64_t clamp_pos(int64_t p, int64_t max_pos) {
 // bounds are multiples of 8) and cos/sin rows are 16-byte aligned, so a unit
 // reads one position and 2 x 32 contiguous bytes of cos/sin.  kPerPair = true:
 // position and cos/sin are read pair by pair (any section bounds, any alignment).
-template <bool kPerPair, bool kNt>
+template <bool kPerPair, int kSt>
 __global__ __launch_bounds__(kThreads) void rope_store_kv_kernel(const RopeArgs a) {
   const int hd = a.head_dim;
   const int half = hd >> 1;
@@ -202,13 +208,13 @@ __global__ __launch_bounds__(kThreads) void rope_store_kv_kernel(const RopeArgs 
                      : (x.kind == 1 ? a.k_cache : a.v_cache) + (int64_t)x.slot * row_elems;
       const bool st0 = x.live && (x.kind == 0 || (store && slot_ok));
       if (st0) {
-        st16<kNt>(dst0 + x.off, lo);
-        st16<kNt>(dst0 + x.off + half, hi);
+        st16<kSt>(dst0 + x.off, lo);
+        st16<kSt>(dst0 + x.off + half, hi);
       }
       if (x.live && x.kind == 1 && a.k_out) {
         uint16_t* dst1 = a.k_out + (int64_t)x.n * a.ko_rs + x.off;
-        st16<kNt>(dst1, lo);
-        st16<kNt>(dst1 + half, hi);
+        st16<kSt>(dst1, lo);
+        st16<kSt>(dst1 + half, hi);
       }
     }
   }
@@ -300,9 +306,14 @@ VLC_API int vlc_rope_store_kvcache(const void* q, int64_t q_row_stride, void* q_
   // bytes written: q_out, the cache's k and v rows, k_out
   const int64_t written = num_tokens * head_dim * 2 *
                           ((int64_t)num_heads_q + (store ? 2 : 0) * num_heads_kv + (k_out ? num_heads_kv : 0));
-  const bool nt = written <= kNtMaxWriteBytes;
-  auto kernel = per_pair ? (nt ? rope_store_kv_kernel<true, true> : rope_store_kv_kernel<true, false>)
-                         : (nt ? rope_store_kv_kernel<false, true> : rope_store_kv_kernel<false, false>);
+  const int mode = store_mode_for(written);
+  auto pick = [&](auto per_pair_c) {
+    constexpr bool kP = decltype(per_pair_c)::value;
+    return mode == kStWt   ? rope_store_kv_kernel<kP, kStWt>
+           : mode == kStNt ? rope_store_kv_kernel<kP, kStNt>
+                           : rope_store_kv_kernel<kP, kStPlain>;
+  };
+  auto kernel = per_pair ? pick(std::true_type{}) : pick(std::false_type{});
   hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), a);
   return launch_status();
 }

@@ -10,11 +10,12 @@
 // 512 B per row) 32 consecutive lanes read and write a whole K row and a whole V
 // row, fully coalesced.  Against one chunk of K or of V per lane this measured
 // 4.89 us against 5.72 us for the 22 MB of a 10741-token layer (2.2 us either
-// way for 1247 tokens, where the launch dominates).  The cache rows are stored
-// nontemporally (streamed to HBM) when the call writes at most kNtMaxWriteBytes:
-// 22 MB in 3.16 against 4.29 us with plain stores, 67 MB in 9.9 against 11.7 us
-// (36 calls in one graph, distinct caches); nontemporal loads as well measured
-// slower (3.4 and 10.4 us).
+// way for 1247 tokens, where the launch dominates).  The cache rows are stored with
+// the policy store_mode_for picks from the bytes the call writes: at agent scope
+// (written through L2) up to 64 MB, nontemporally up to 256 MB (22 MB in 3.16
+// against 4.29 us with plain stores, 67 MB in 9.9 against 11.7 us; 36 calls in one
+// graph, distinct caches), plain above; nontemporal loads measured slower (3.4 and
+// 10.4 us).
 #include "common.h"
 
 namespace vlc {
@@ -22,7 +23,7 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <bool kNt>
+template <int kSt>
 __global__ __launch_bounds__(kThreads) void store_kvcache_vec16(
     const char* __restrict__ key, int64_t key_stride_b, const char* __restrict__ value,
     int64_t value_stride_b, char* __restrict__ k_cache, char* __restrict__ v_cache,
@@ -45,8 +46,8 @@ __global__ __launch_bounds__(kThreads) void store_kvcache_vec16(
                  "v"(vd.w));
     if (slot < 0 || slot >= num_slots) continue;
     const int64_t o = (int64_t)slot * row_bytes + (int64_t)cc * 16;
-    st16<kNt>(k_cache + o, kd);
-    st16<kNt>(v_cache + o, vd);
+    st16<kSt>(k_cache + o, kd);
+    st16<kSt>(v_cache + o, vd);
   }
 }
 
@@ -98,8 +99,10 @@ VLC_API int vlc_store_kvcache(const void* key, int64_t key_row_stride, const voi
     int64_t blocks = (total + kThreads - 1) / kThreads;
     if (blocks < 1) blocks = 1;
     if (blocks > (1 << 20)) blocks = 1 << 20;
-    auto kernel = 2 * num_tokens * row_bytes <= kNtMaxWriteBytes ? store_kvcache_vec16<true>
-                                                                  : store_kvcache_vec16<false>;
+    const int mode = store_mode_for(2 * num_tokens * row_bytes);
+    auto kernel = mode == kStWt   ? store_kvcache_vec16<kStWt>
+                  : mode == kStNt ? store_kvcache_vec16<kStNt>
+                                  : store_kvcache_vec16<kStPlain>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s,
                        static_cast<const char*>(key), key_row_stride * elem_bytes,
                        static_cast<const char*>(value), value_row_stride * elem_bytes,
