@@ -179,10 +179,7 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
 // loads in its waits, so their results are used only after an explicit vmcnt(0)
 // that takes them as operands.
 __device__ __forceinline__ void st16_agent(void* addr, f32x4 v) {
-  // s_nop 1: two wait states before a VALU write of the data registers, which the
-  // compiler reuses right after this statement (it does not track the hazard of a
-  // store of more than 8 bytes through inline assembly).
-  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(addr), "v"(v) : "memory");
+  st16_wt(addr, __builtin_bit_cast(u32x4_vec, v));
 }
 __device__ __forceinline__ f32x4 ld16_agent(const void* addr) {
   f32x4 v;
@@ -190,8 +187,7 @@ __device__ __forceinline__ f32x4 ld16_agent(const void* addr) {
   return v;
 }
 __device__ __forceinline__ void st_ml_agent(float* addr, float m, float l) {
-  const uint64_t bits = (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(l) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(addr), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  st8_wt(addr, (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(l) << 32));
 }
 __device__ __forceinline__ float2 ld_ml_agent(const float* addr) {
   const uint64_t bits =
