@@ -130,3 +130,44 @@ def test_eight_requests_sharing_one_image(dev):
     o_ref = oattn.varlen_attention(q_ref, ref[0, 1], ref[1, 1], hp.cu_q_host, hp.cu_k_host, hp.scale, True,
                                    hp.block_tables.cpu().tolist(), 256)
     assert_attn_close(out, o_ref, what="8-request attention")
+
+
+def test_4k_warm_request_graph_replays_match_eager(dev):
+    """The warm request's per-layer calls (fused M-RoPE + KV store, then attention with its
+    split-KV merge) for four layers captured as one HIP graph, as bench.py replays them, and
+    replayed three times with eager calls of other layers in between (they rewrite the shared
+    rotated q and the plan's split workspace).  Every replay's outputs equal the eager outputs
+    bit for bit; the outputs are cleared by a fill kernel before each replay."""
+    say("graph: 4K warm request, 4 layers of rope_store + attention, 3 replays vs eager")
+    hp = WarmPrefillHotPath(workloads.cfg2(), dev, seed=0)
+    layers = [0, 7, 19, 35]
+
+    def run(outs):
+        for l, o in zip(layers, outs):
+            hp.rope_store(l)
+            kernels.varlen_attention(hp.q, hp.k_caches[l], hp.v_caches[l], hp.cu_q, hp.cu_k, hp.scale, True,
+                                     hp.block_tables, plan=hp.plan, out=o)
+
+    eager = [torch.empty_like(hp.out) for _ in layers]
+    run(eager)
+    torch.cuda.synchronize()
+    ref = [e.clone() for e in eager]
+    outs = [torch.empty_like(hp.out) for _ in layers]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(outs)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(outs)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        for l in (3, 11, 28):  # eager work on the same q, workspace and plan
+            hp.rope_store(l)
+            hp.attention(l)
+        g.replay()
+        torch.cuda.synchronize()
+        for l, o, r in zip(layers, outs, ref):
+            assert torch.equal(o, r), f"replay {rep}, layer {l}"
