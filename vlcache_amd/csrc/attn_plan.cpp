@@ -77,10 +77,12 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
   };
   std::vector<Tile> tiles;
   int64_t total = 0;
+  bool reused_context = false;
   for (int b = 0; b < num_seqs; ++b) {
     const int64_t sq = (int64_t)cu_q[b + 1] - cu_q[b];
     const int64_t sk = (int64_t)cu_k[b + 1] - cu_k[b];
     if (sq < 0 || sk < 0 || cu_q[b] < 0 || cu_k[b] < 0) return VLC_ERR_INVALID;
+    reused_context = reused_context || sk > sq;
     for (int64_t qs = 0; qs < sq; qs += ppt) {
       const int qc = (int)std::min<int64_t>(ppt, sq - qs);
       int64_t kmax = sk;
@@ -157,6 +159,7 @@ VLC_HOST_API int vlc_attn_plan(const int32_t* cu_q, const int32_t* cu_k, int num
   plan[kPNumHeadsKv] = num_heads_kv;
   plan[kPCausal] = causal ? 1 : 0;
   plan[kPHeadDim] = head_dim;
+  plan[kPAltPrio] = reused_context ? 1 : 0;
   int32_t* w = plan + kHeaderInts;
   for (const Item& it : items) { std::memcpy(w, it.v, sizeof(it.v)); w += kItemInts; }
   for (const Item& c : combines) { std::memcpy(w, c.v, sizeof(c.v)); w += kItemInts; }

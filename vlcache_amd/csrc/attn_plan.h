@@ -33,6 +33,7 @@ enum PlanField {
   kPNumHeadsKv = 8,
   kPCausal = 9,
   kPHeadDim = 10,
+  kPAltPrio = 11,  // 1: some sub-sequence has more keys than queries (reused context)
 };
 
 // Work item (int32 x 16): one workgroup.
