@@ -211,3 +211,13 @@ def test_decode_noalloc_refuses_calls_beyond_its_scratch(lib):
     plan = kernels.plan_decode(B, hq, hkv, 128, 256, 2048, "cpu", num_splits=2, workspace=False)
     assert plan.grid_splits == 2 and plan.workspace is None
     assert plan.workspace_bytes > _lib.DECODE_NOALLOC_MAX_BYTES
+
+
+def test_plan_flags_reused_context():
+    """Header word 11 (kPAltPrio) is 1 exactly when some sub-sequence has more keys than
+    queries: the paged kernels then alternate wave priorities between steps."""
+    warm = kernels.plan_attention([0, 1183, 1247], [0, 1183, 11924], 16, 2, 128, True, "cpu", num_cus=256)
+    square = kernels.plan_attention([0, 4096], [0, 4096], 16, 2, 128, True, "cpu", num_cus=256)
+    batch = kernels.plan_attention([0, 10, 30, 40], [0, 10, 30, 40], 28, 4, 128, True, "cpu", num_cus=256)
+    one_longer = kernels.plan_attention([0, 10, 30], [0, 10, 31], 28, 4, 128, True, "cpu", num_cus=256)
+    assert [int(p.host[11]) for p in (warm, square, batch, one_longer)] == [1, 0, 0, 1]
