@@ -678,8 +678,8 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
 // loaded together with the maxima: one round trip instead of two.
 constexpr int kCombineCols = kThreads / (kHeadDim / 8);  // 16 columns per workgroup
 
-// Weighted sum of one column slice over the splits: acc = sum_s w_s Ohat_s and the
-// return value sum_s w_s, w_s = 2^(m_s - M) l_s.  The 16 lanes of a column form one
+// Weighted sum of one column slice over the splits: a.acc += sum_s w_s Ohat_s and
+// a.lsum += sum_s w_s, w_s = 2^(m_s - M) l_s.  The 16 lanes of a column form one
 // DPP row: lane j loads (m, l) of splits j, j + 16, j + 32, j + 48 of each chunk of 64,
 // computes their weights, and a row broadcast (row_newbcast) hands w_s to the row when
 // split s is accumulated, so (m, l) is loaded once per split and column instead of
