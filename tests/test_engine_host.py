@@ -368,6 +368,36 @@ def test_encoder_cache_lru_views_and_limits():
     assert not ec2.put(9, torch.zeros(9, 1))  # larger than the pool: not cached
 
 
+def test_process_visual_hits_survive_evictions_by_the_same_step():
+    """A step reads image A from the cache (a view of the pool) and then stores the
+    miss B, which evicts A and reuses its pages.  A's rows in the step's embeddings
+    must still be A's: the reference's read gathers a copy
+    (engine/encoder_cache_manager.py:59-62)."""
+    from types import SimpleNamespace
+
+    from vlcache_amd.engine.encoder_cache import EncoderCache
+    from vlcache_amd.engine.model_runner import ModelRunner
+
+    hidden = 3
+    ec = EncoderCache(num_pages=2, page_rows=2, hidden=hidden, dtype=torch.float32, device="cpu")
+    a = torch.arange(4 * hidden, dtype=torch.float32).view(4, hidden) + 1.0  # grid (1, 4, 4): 4 rows
+    b = torch.full((4, hidden), -7.0)
+    assert ec.put(11, a)
+    cfg = SimpleNamespace(hf_config=SimpleNamespace(hidden_size=hidden, spatial_merge_size=2),
+                          synthetic_vision=False)
+    stub = SimpleNamespace(encoder_cache=ec, config=cfg, dtype=torch.float32, device=torch.device("cpu"),
+                           model=SimpleNamespace(visual=None))
+    stub._num_units = lambda grid: ModelRunner._num_units(stub, grid)
+    mm = dict(image_hashes=[11, 22], image_grid_thw=[(1, 4, 4), (1, 4, 4)], image_embeds=[None, b],
+              pixel_values=[None, None], recompute=[3, 0])
+    out, vit = ModelRunner._process_visual(stub, mm)
+    assert vit == 0.0 and ec.hits == 1 and 11 not in ec and 22 in ec and ec.evictions == 1
+    assert torch.equal(out[:3], a[:3]), "the hit's rows were overwritten by the same step's put"
+    assert torch.equal(out[3:], b)
+    # the evicted image's pages now hold B
+    assert torch.equal(ec.get(22), b)
+
+
 def test_runner_refuses_token_ids_outside_the_vocabulary():
     from types import SimpleNamespace
 

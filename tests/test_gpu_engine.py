@@ -387,6 +387,46 @@ def test_decode_graph_replays_match_the_eager_decode(dev):
     assert set(runner._graphs) == {1, 2, 4}
 
 
+def test_decode_graph_capture_leaves_other_requests_kv_alone(dev):
+    """Capturing the decode graph of a new batch size runs the decoder once eagerly on the
+    static buffers.  After earlier replays those buffers still hold a finished request's
+    slots and block tables, whose blocks a new request may own by then.  The capture must
+    not store into them: the new request's KV bytes are the same before and after it."""
+    from vlcache_amd import LLM
+
+    say("engine: decode-graph capture of a new batch size over stale static buffers")
+    eng = LLM(dict(TINY), recompute_ratio=0.1, num_kvcache_blocks=16, max_model_len=2048, seed=5,
+              synthetic_vision=True, enforce_eager=False, max_num_seqs=8)
+    runner = eng.model_runner
+    rng = np.random.default_rng(2)
+    seq = eng.add_request([int(x) for x in rng.integers(1, 900, 300)],
+                          SamplingParams(temperature=1.0, max_tokens=4, ignore_eos=True), None)
+    seqs, is_prefill = eng.scheduler.schedule()
+    assert is_prefill and seqs == [seq]
+    runner.run(seqs, True)
+    torch.cuda.synchronize()
+    bt = list(seq.block_table)
+    page = runner.block_size
+    prompt_slots = [bt[p // page] * page + p % page for p in range(len(seq))]
+    # what a replay of an earlier batch left in rows 0..3 of the static buffers: decode
+    # rows that wrote to (and read through) blocks this request now owns
+    gv = runner._graph_static()
+    gv["input_ids"][:4] = torch.tensor([17, 18, 19, 20], device=dev)
+    gv["positions"][:, :4] = torch.tensor([5, 77, 150, 299], device=dev)
+    gv["slot_mapping"][:4] = torch.tensor([prompt_slots[i] for i in (5, 77, 150, 299)], dtype=torch.int32,
+                                          device=dev)
+    gv["context_lens"][:4] = torch.tensor([6, 78, 151, 300], dtype=torch.int32, device=dev)
+    gv["block_tables"][:4, :len(bt)] = torch.tensor(bt, dtype=torch.int32, device=dev)
+    before = runner.kv_cache.clone()
+    assert 4 not in runner._graphs
+    with torch.inference_mode():
+        runner._capture_decode_graph(4)
+    torch.cuda.synchronize()
+    assert torch.equal(runner.kv_cache.view(torch.int16), before.view(torch.int16)), \
+        "the capture's warm-up run stored into another request's KV slots"
+    reset_context()
+
+
 def test_partial_warm_ttft_below_nine_tenths_of_full_recompute(dev):
     """The reference's pass rule (test_partial_recompute.py:151-152): the warm request's TTFT with
     recompute_ratio=0.1 is below 0.9 x its TTFT with recompute_ratio=0.0 (full recompute).

@@ -53,7 +53,11 @@ class EncoderCache:
         return -(-rows // self.page_rows)
 
     def get(self, key: int, rows: int | None = None) -> torch.Tensor | None:
-        """The first `rows` embeddings of an image (all when None), or None on a miss."""
+        """The first `rows` embeddings of an image (all when None), or None on a miss.
+
+        The result may be a view of the pool: it holds the image's rows only until the
+        next put(), which can evict the entry and reuse its pages.  Copy it before then.
+        """
         entry = self._entries.get(key)
         if entry is None:
             self.misses += 1

@@ -326,7 +326,23 @@ class ModelRunner:
         Config.synthetic_vision opts in and raises otherwise.
         """
         hashes, grids = mm["image_hashes"], mm["image_grid_thw"]
-        out: list = [None] * len(hashes)
+        if not hashes:
+            return None, 0.0
+        # Rows each image contributes, and their place in the output.  Every result is
+        # copied into its slice as soon as it is known: a cache hit is a view of the
+        # pool, and a later put() of this call may evict that entry and reuse its pages.
+        sizes = []
+        for grid, r in zip(grids, mm["recompute"]):
+            n = self._num_units(grid)
+            sizes.append(min(int(r), n) if r > 0 else n)
+        offs = np.concatenate([[0], np.cumsum(sizes)]).tolist()
+        out = torch.empty(offs[-1], self.config.hf_config.hidden_size, dtype=self.dtype, device=self.device)
+
+        def place(i, emb):
+            if emb.shape[0] < sizes[i]:
+                raise ValueError(f"image {i}: {emb.shape[0]} embedding rows, {sizes[i]} needed")
+            out[offs[i]:offs[i + 1]].copy_(emb[:sizes[i]])
+
         run: dict[int, list[int]] = {}          # hash -> indices waiting for the vision tower
         vit_time = 0.0
         for i, (h, grid, given, pix, r) in enumerate(zip(hashes, grids, mm["image_embeds"], mm["pixel_values"],
@@ -334,7 +350,7 @@ class ModelRunner:
             rows = r if r > 0 else None
             hit = self.encoder_cache.get(h, rows)
             if hit is not None:
-                out[i] = hit
+                place(i, hit)
                 continue
             n = self._num_units(grid)
             if given is not None:
@@ -357,8 +373,8 @@ class ModelRunner:
                 raise RuntimeError(f"image {h:#x} is not in the encoder cache and {why}")
             if emb.shape[0] != n:
                 raise ValueError(f"image_embeds has {emb.shape[0]} rows, the grid {tuple(grid)} gives {n}")
+            place(i, emb)
             self.encoder_cache.put(h, emb)
-            out[i] = emb if rows is None else emb[:rows]
         if run:
             first = [idx[0] for idx in run.values()]
             pv = torch.cat([mm["pixel_values"][i].to(self.device) for i in first], dim=0)
@@ -368,11 +384,10 @@ class ModelRunner:
             torch.cuda.synchronize(self.device)
             vit_time = perf_counter() - t0
             for (h, idx), emb in zip(run.items(), torch.split(emb_all, [self._num_units(grids[i]) for i in first])):
-                self.encoder_cache.put(h, emb)
                 for i in idx:
-                    r = mm["recompute"][i]
-                    out[i] = emb if r <= 0 else emb[:r]
-        return (torch.cat(out, dim=0) if out else None), vit_time
+                    place(i, emb)
+                self.encoder_cache.put(h, emb)
+        return out, vit_time
 
     # ------------------------------------------------------------------ decode graphs
     # With enforce_eager=False a decode step replays a HIP graph of the model's decode
@@ -424,9 +439,17 @@ class ModelRunner:
 
     def _capture_decode_graph(self, bs: int):
         gv = self._graph_static()
+        # The warm-up run below executes: put its rows in the padding state first (no
+        # slot stored, empty contexts).  After earlier replays the static buffers still
+        # hold a previous step's slots and block tables, whose blocks may belong to
+        # another request by now.
+        gv["input_ids"][:bs].zero_()
+        gv["positions"][:, :bs].zero_()
+        gv["slot_mapping"][:bs].fill_(-1)
+        gv["context_lens"][:bs].zero_()
+        gv["block_tables"][:bs].fill_(-1)
         self._graph_context(bs)
         ids, pos = gv["input_ids"][:bs], self._graph_positions(bs)
-        # one eager run on the capture inputs (padding state: nothing stored, empty contexts)
         gv["outputs"][:bs] = self.model(ids, pos)
         torch.cuda.synchronize(self.device)
         g = torch.cuda.CUDAGraph()
