@@ -156,7 +156,9 @@ int vlc_attn_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
  *
  * q: [total_q, num_heads_q, head_dim], row stride q_row_stride elements.
  * Paged mode (block_table != NULL): k/v are caches [num_blocks, page_size,
- *   num_heads_kv, head_dim]; key j of sequence b lives in row
+ *   num_heads_kv, head_dim], page_size a multiple of 16 (VLC_ERR_UNSUPPORTED
+ *   otherwise; the reference's pages are multiples of 256, config.py:24); key j of
+ *   sequence b lives in row
  *   block_table[b*bt_row_stride + j/page_size]*page_size + j%page_size;
  *   k_row_stride/v_row_stride are elements per cache row.  A block id outside
  *   [0, num_blocks) reads as zeros (it is never dereferenced).

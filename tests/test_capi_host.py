@@ -221,3 +221,19 @@ def test_plan_flags_reused_context():
     batch = kernels.plan_attention([0, 10, 30, 40], [0, 10, 30, 40], 28, 4, 128, True, "cpu", num_cus=256)
     one_longer = kernels.plan_attention([0, 10, 30], [0, 10, 31], 28, 4, 128, True, "cpu", num_cus=256)
     assert [int(p.host[11]) for p in (warm, square, batch, one_longer)] == [1, 0, 0, 1]
+
+
+def test_paged_attention_refuses_pages_not_multiple_of_16(lib):
+    """Paged attention loads 16 consecutive keys per wave and tile from one page, so a
+    page size that is not a multiple of 16 is refused before any device work (the
+    reference's pages are multiples of 256, config.py:24)."""
+    cu_q, cu_k = [0, 40], [0, 100]
+    plan = kernels.plan_attention(cu_q, cu_k, 16, 2, 128, True, "cpu")
+    ip = ctypes.POINTER(ctypes.c_int32)
+    fake = 1 << 20  # 16-byte aligned stand-in addresses: the call must return before using them
+    for page, want in ((8, -2), (24, -2), (100, -2)):
+        st = lib.vlc_varlen_attn_fwd(fake, 16 * 128, fake, 2 * 128 * 1, fake, 2 * 128, fake, 8, page, 64,
+                                     fake, fake, 1, 16, 2, 128, 128 ** -0.5, 1,
+                                     plan.host.ctypes.data_as(ip), fake, plan.host.size,
+                                     fake, 16 * 128, fake, 1 << 30, None)
+        assert st == want, (page, st)

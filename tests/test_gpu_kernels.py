@@ -485,15 +485,18 @@ def test_attention_random_shapes(dev, seed):
     assert_attn_close(out, ref, what=f"random attention seed {seed}")
 
 
-def test_attention_small_pages_and_non_causal(dev):
-    say("attention: page size 16 (per-row lookup), causal and non-causal")
-    subs = [(40, 100), (7, 7), (64, 64)]
+@pytest.mark.parametrize("page", [16, 32, 48, 80])
+def test_attention_small_pages_and_non_causal(dev, page):
+    """Pages that are multiples of 16 but not of 64: each wave's 16 rows of a tile lie in
+    one page (48 and 80 put page boundaries inside tiles), causal and non-causal."""
+    say(f"attention: page size {page} (per-wave page lookup), causal and non-causal")
+    subs = [(40, 100), (7, 7), (64, 64), (130, 700)]
     hq, hkv = 8, 1
-    q, kc, vc, bt, cu_q, cu_k = _paged_case(23, hq, hkv, subs, page=16)
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(23, hq, hkv, subs, page=page)
     for causal in (True, False):
         out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=causal)
-        ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), 16)
-        assert_attn_close(out, ref, what=f"page-16 causal={causal}")
+        ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), page)
+        assert_attn_close(out, ref, what=f"page-{page} causal={causal}")
 
 
 def test_attention_rows_without_keys_are_zero(dev):

@@ -82,21 +82,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Physical row of key `key` of sequence b through the block table, or -1 when the
-// key is past the sequence or its block id is outside the cache.
-__device__ __forceinline__ int64_t paged_row_of(const Params& p, int b, int sk, int key) {
-  const int kc = min(key, sk - 1);
-  const int pg = kc / p.page_size;
-  const int32_t blk = p.block_table[(int64_t)b * p.bt_row_stride + pg];
-  const bool ok = key < sk && blk >= 0 && blk < p.num_blocks;
-  return ok ? (int64_t)blk * p.page_size + (kc - pg * p.page_size) : -1;
-}
-
 // How keys map to rows of k/v.
 enum KvMode {
   kContiguous = 0,  // key j of sequence b is row cu_k[b] + j
   kPagedTiles = 1,  // paged, page_size % 64 == 0: a 64-key tile lies inside one page
-  kPagedRows = 2,   // paged, any page size: one block-table lookup per row
+  kPagedRows = 2,   // paged, page_size % 16 == 0: the 16 rows a wave loads lie inside one page
 };
 
 // Online-softmax threshold (log2 units): the running max only moves when a tile's
@@ -275,41 +265,6 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
   const uint32_t lchunk0 = (uint32_t)((lane & 15) ^ ((lane >> 4) << 2));
   const char* zero = reinterpret_cast<const char*>(kZeroRow);
 
-  // Loads tile u of the item into an LDS buffer, without a branch: tiles past the
-  // item and pages outside the cache read the zero row; rows past the sequence
-  // read its last row (their keys are masked, so the products never use them).
-  auto dma_tile = [&](int u, uint8_t* dst, const char* colbase, int64_t st) __attribute__((always_inline)) {
-    const int kt = k_begin + u * kTileK;
-    const uint32_t lr = opaque(lrow0), lcn = opaque(lchunk0);
-    if (MODE == kPagedRows) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int lrow = (int)lr + 4 * j;
-        const uint32_t lchunk = (lcn ^ (uint32_t)j) << 4;
-        const int64_t pr = u < n_tiles ? paged_row_of(p, b, sk, kt + lrow) : -1;
-        const char* src = pr >= 0 ? colbase + pr * st + lchunk : zero + lchunk;
-        dma16_addr(src, lds_u32(dst + (16 * wave + 4 * j) * 256));
-      }
-      return;
-    }
-    const bool in = u < n_tiles;
-    int64_t row0;
-    bool ok = in;
-    if (MODE == kContiguous) {
-      row0 = (int64_t)k0 + kt;
-    } else {
-      const int32_t blk = __builtin_amdgcn_readfirstlane(tile_blk[min(u, max(n_tiles - 1, 0))]);
-      ok = ok && blk >= 0 && blk < p.num_blocks;
-      row0 = (int64_t)blk * p.page_size + (kt % p.page_size);
-    }
-    const char* tb = ok ? colbase + row0 * st : zero;
-    const uint32_t last = ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u;  // last row to read
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      dma16(tb, min(lr + 4 * j, last) * (uint32_t)st + ((lcn ^ (uint32_t)j) << 4),
-            lds_u32(dst + (16 * wave + 4 * j) * 256));
-  };
-
   // ---- state ---------------------------------------------------------------------
   f32x16 o[4];
 #pragma unroll
@@ -356,28 +311,42 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     }
   };
 
-  // Sources of one tile load: a uniform base and the last row to read (see dma_tile).
+  // Source of one tile load: a uniform base and the last row to read.  Lane row r
+  // (lrow0 + 4j) reads base + min(r, last) rows: rows past the sequence read its last
+  // row (their keys are masked, so the products never use them); tiles past the item
+  // and pages outside the cache read the zero row (last = 0).
   struct DmaSrc {
     const char* base;
     uint32_t last;
   };
-  // direct: read the block id from the block table (scalar load) instead of the
-  // LDS copy, for the prologue, which does not wait for that copy.
+  // Paged tiles: the tile's block id, from the LDS copy of the item's page table, or
+  // with `direct` from the block table (scalar load), for the prologue, which does not
+  // wait for that copy.  Paged rows: the block id of the wave's 16 rows (one page,
+  // page_size % 16 == 0), a scalar load of the block table; base is then that page
+  // row minus the wave's first tile row, so lane row r still reads base + r rows.
+  typedef const __attribute__((address_space(4))) int32_t* const_i32p;
   auto dma_src = [&](int u, const char* colbase, int64_t st, bool direct = false) __attribute__((always_inline)) {
     const int kt = k_begin + u * kTileK;
-    int64_t row0;
     bool ok = u < n_tiles;
     if (MODE == kContiguous) {
-      row0 = (int64_t)k0 + kt;
-    } else {
-      typedef const __attribute__((address_space(4))) int32_t* const_i32p;
-      const int32_t blk =
-          direct ? (ok ? ((const_i32p)(uintptr_t)(p.block_table + (int64_t)b * p.bt_row_stride))[kt / p.page_size] : 0)
-                 : __builtin_amdgcn_readfirstlane(tile_blk[min(u, max(n_tiles - 1, 0))]);
-      ok = ok && blk >= 0 && blk < p.num_blocks;
-      row0 = (int64_t)blk * p.page_size + (kt % p.page_size);
+      const int64_t row0 = (int64_t)k0 + kt;
+      return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u};
     }
-    return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u};
+    const const_i32p bt_row = (const_i32p)(uintptr_t)(p.block_table + (int64_t)b * p.bt_row_stride);
+    if (MODE == kPagedTiles) {
+      const int32_t blk = direct ? (ok ? bt_row[kt / p.page_size] : 0)
+                                 : __builtin_amdgcn_readfirstlane(tile_blk[min(u, max(n_tiles - 1, 0))]);
+      ok = ok && blk >= 0 && blk < p.num_blocks;
+      const int64_t row0 = (int64_t)blk * p.page_size + (kt % p.page_size);
+      return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u};
+    }
+    const int g0 = kt + 16 * wave;  // first key of the wave's rows
+    ok = ok && g0 < sk;
+    const int pg = g0 / p.page_size;
+    const int32_t blk = ok ? bt_row[pg] : 0;
+    ok = ok && blk >= 0 && blk < p.num_blocks;
+    const int64_t row0 = (int64_t)blk * p.page_size + (g0 - pg * p.page_size) - 16 * wave;
+    return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)(16 * wave + min(15, sk - 1 - g0)) : 0u};
   };
 
   // O^T += V^T P^T of the last tile, reads a few MFMAs ahead (sched groups: 0x008
@@ -485,19 +454,14 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     for (int i = 0; i < NU; ++i) {
       if (i + kAhead < NU) read_op(i + kAhead);
       mfma_op(i);
-      if (MODE != kPagedRows) {
-        // row (< 64) x row stride (< 2^24 bytes, checked on the host): a 24-bit multiply-add
-        if (i < 4) {
-          dma16(dk.base, __umul24(min(lr + 4 * i, dk.last), (uint32_t)kst) + ((lcn ^ (uint32_t)i) << 4),
-                lds_u32(k_ld + (16 * wave + 4 * i) * 256));
-        } else if (i < 8) {
-          const int r = i - 4;
-          dma16(dv.base, __umul24(min(lr + 4 * r, dv.last), (uint32_t)vst) + ((lcn ^ (uint32_t)r) << 4),
-                lds_u32(v_ld + (16 * wave + 4 * r) * 256));
-        }
-      } else {
-        if (i == 0) dma_tile(t + 2, k_ld, kcol, kst);
-        if (i == 1) dma_tile(t, v_ld, vcol, vst);
+      // row (< 64) x row stride (< 2^24 bytes, checked on the host): a 24-bit multiply-add
+      if (i < 4) {
+        dma16(dk.base, __umul24(min(lr + 4 * i, dk.last), (uint32_t)kst) + ((lcn ^ (uint32_t)i) << 4),
+              lds_u32(k_ld + (16 * wave + 4 * i) * 256));
+      } else if (i < 8) {
+        const int r = i - 4;
+        dma16(dv.base, __umul24(min(lr + 4 * r, dv.last), (uint32_t)vst) + ((lcn ^ (uint32_t)r) << 4),
+              lds_u32(v_ld + (16 * wave + 4 * r) * 256));
       }
       if (i < 3) {  // mask and partial max of elements 11i .. 11i+10
 #pragma unroll
@@ -565,10 +529,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) pk[kb][ch] = __builtin_bit_cast(bf16x8, u32x4v{0u, 0u, 0u, 0u});
-    if (MODE == kPagedRows) {
-      dma_tile(0, k_buf0, kcol, kst);
-      dma_tile(1, k_buf1, kcol, kst);
-    } else {
+    {
       const DmaSrc d0 = dma_src(0, kcol, kst, true), d1 = dma_src(1, kcol, kst, true);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -870,6 +831,8 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
       k_row_stride < (int64_t)num_heads_kv * kHeadDim || v_row_stride < (int64_t)num_heads_kv * kHeadDim)
     return VLC_ERR_INVALID;
   if (block_table && (page_size <= 0 || bt_row_stride <= 0 || num_blocks <= 0)) return VLC_ERR_INVALID;
+  // Paged K/V: a wave loads 16 consecutive keys of a tile, which must share a page.
+  if (block_table && page_size % 16 != 0) return VLC_ERR_UNSUPPORTED;
   if (n_slots > 0 && (!workspace || workspace_bytes < n_slots * kSlotBytes || !aligned16(workspace)))
     return VLC_ERR_WORKSPACE;
 
