@@ -21,7 +21,7 @@
 // a head, so for 2 kv heads x 128 dims one token row (512 B) is 16 consecutive
 // lanes.  A lane moves the same unit of K and of V (four 16-byte loads in flight,
 // one slot lookup for both, then four 16-byte stores).  grid.y walks layers;
-// grid.x walks tokens, one unit per lane, 512-lane workgroups.  Against one
+// grid.x walks tokens, one unit per lane (see kStreamThreads).  Against one
 // plane per lane in 256-lane workgroups this measured 114 us against 129 us for
 // the 700 MB of the 4K-image request (clean MALL) and 831 against 956 us for
 // 5.9 GB; more layers per lane (fewer workgroups) measured slower.
@@ -30,7 +30,11 @@
 namespace vlc {
 namespace {
 
-constexpr int kThreads = 512;
+// Workgroup size: 256 lanes for calls that stream past the MALL (124.9 against
+// 125.9 us at 512 with a dirty MALL, 124.4 against 125.2 clean, on the 0.70 GB call),
+// 512 for the larger calls (831 against 856 us at 256 on 5.9 GB).
+constexpr int kStreamThreads = 256;
+constexpr int kPlainThreads = 512;
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void rotate_word(uint32_t& a, uint32_t& b, float2 cs0, float2 cs1) {
@@ -55,17 +59,25 @@ __device__ __forceinline__ void rotate_word(uint32_t& a, uint32_t& b, float2 cs0
   b = yb0 | (yb1 << 16);
 }
 
-// Loads: kNtLoad = true issues them nontemporal (not kept in the MALL).  Measured
-// with K and V per lane (cold, clean / dirty MALL): 0.74 GB moved, 115 / 146 us
-// against 122 / 166 us plain; 1.48 GB, 242 / 283 against 222 / 253 us; 5.9 GB,
-// 1091 / 1128 against 855 / 883 us.  The host picks nontemporal loads up to
-// kNtLoadMaxBytes moved (read + write) and plain ones above.  The same calls store
-// through L2 (st16_wt), which leaves no dirty lines for the write-back at the
-// kernel's end: 0.70 GB in 107.6 / 131.6 us against 109.8 / 135.4 us with plain
-// stores; at 5.9 GB such stores measured 0.9 % slower, so larger calls keep plain ones.
-constexpr int64_t kNtLoadMaxBytes = (int64_t)1 << 30;
+// Calls that move at most kStreamMaxBytes (read + write) stream past the MALL: loads
+// nontemporal and stores at agent scope with the nontemporal hint (st16_wt_nt, written
+// through L2 and not allocated in the MALL).  The warm request's call meets a MALL full
+// of the previous request's dirty KV lines; any access that allocates there first
+// writes those back.  Measured on the 4K request's 0.70 GB (cold, median, clean / dirty
+// MALL, us): nontemporal loads with these stores 124.8 / 124.8; with agent-scope
+// stores that allocate 108.3 / 132.5; nontemporal stores 125.5 / 125.4; plain loads and
+// stores 116.3 / 159.6.  Larger calls (1.48 GB and up) use plain loads and stores, which
+// stream faster once the MALL's contents are a small part of the call: 5.9 GB in
+// 855 / 883 us against 1091 / 1128 us with nontemporal loads.
+constexpr int64_t kStreamMaxBytes = (int64_t)1 << 30;
 
-template <bool kNtLoad>
+// 16-byte store at agent scope with the nontemporal hint; same inline-assembly caveats
+// as st16_wt.
+__device__ __forceinline__ void st16_wt_nt(void* p, const u32x4_vec& w) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1 nt\n\ts_nop 1" : : "v"(p), "v"(w) : "memory");
+}
+
+template <bool kStream, int kThreads = kStream ? kStreamThreads : kPlainThreads>
 __global__ __launch_bounds__(kThreads) void rerotate_copy_kv_kernel(
     uint16_t* __restrict__ kv, int64_t plane_stride, int64_t layer_stride, int num_layers,
     const int64_t* __restrict__ old_slots, const int64_t* __restrict__ new_slots,
@@ -100,8 +112,8 @@ __global__ __launch_bounds__(kThreads) void rerotate_copy_kv_kernel(
     const uint16_t* src = base + os * row_elems + off;
     const u32x4v* s0 = reinterpret_cast<const u32x4v*>(src);
     const u32x4v* s1 = reinterpret_cast<const u32x4v*>(src + half);
-    u32x4 lo = __builtin_bit_cast(u32x4, kNtLoad ? __builtin_nontemporal_load(s0) : *s0);
-    u32x4 hi = __builtin_bit_cast(u32x4, kNtLoad ? __builtin_nontemporal_load(s1) : *s1);
+    u32x4 lo = __builtin_bit_cast(u32x4, kStream ? __builtin_nontemporal_load(s0) : *s0);
+    u32x4 hi = __builtin_bit_cast(u32x4, kStream ? __builtin_nontemporal_load(s1) : *s1);
     if (rot) {
       int sgi = seg_of_token ? seg_of_token[n] : 0;
       sgi = sgi < 0 ? 0 : (sgi >= num_segments ? num_segments - 1 : sgi);
@@ -123,9 +135,9 @@ __global__ __launch_bounds__(kThreads) void rerotate_copy_kv_kernel(
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       if (un[k].dst) {
-        if constexpr (kNtLoad) {
-          st16_wt(un[k].dst, __builtin_bit_cast(u32x4_vec, un[k].lo));
-          st16_wt(un[k].dst + half, __builtin_bit_cast(u32x4_vec, un[k].hi));
+        if constexpr (kStream) {
+          st16_wt_nt(un[k].dst, __builtin_bit_cast(u32x4_vec, un[k].lo));
+          st16_wt_nt(un[k].dst + half, __builtin_bit_cast(u32x4_vec, un[k].hi));
         } else {
           *reinterpret_cast<u32x4v*>(un[k].dst) = __builtin_bit_cast(u32x4v, un[k].lo);
           *reinterpret_cast<u32x4v*>(un[k].dst + half) = __builtin_bit_cast(u32x4v, un[k].hi);
@@ -158,11 +170,13 @@ VLC_API int vlc_rerotate_copy_kv(void* kv_cache, int64_t plane_stride, int64_t l
   const int units_per_token = num_kv_heads * (head_dim / 16);
   const int64_t total = num_tokens * units_per_token;
   if (total >= ((int64_t)1 << 32)) return VLC_ERR_UNSUPPORTED;  // 32-bit unit index
-  int64_t bx = (total + kThreads - 1) / kThreads;
-  if (bx > 65535) bx = 65535;
   const int64_t moved = num_tokens * num_layers * 2 * (int64_t)row_elems * 2 * 2;  // K+V, read+write
-  auto kernel = moved <= kNtLoadMaxBytes ? rerotate_copy_kv_kernel<true> : rerotate_copy_kv_kernel<false>;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)bx, num_layers), dim3(kThreads), 0,
+  const bool past_mall = moved <= kStreamMaxBytes;
+  const int threads = past_mall ? kStreamThreads : kPlainThreads;
+  int64_t bx = (total + threads - 1) / threads;
+  if (bx > 65535) bx = 65535;
+  auto kernel = past_mall ? rerotate_copy_kv_kernel<true> : rerotate_copy_kv_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)bx, num_layers), dim3(threads), 0,
                      as_stream(stream), static_cast<uint16_t*>(kv_cache), plane_stride, layer_stride,
                      num_layers, old_slots, new_slots, num_tokens, num_slots, row_elems, head_dim,
                      units_per_token, seg_of_token, reinterpret_cast<const float2*>(cos_sin),
