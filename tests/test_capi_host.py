@@ -213,14 +213,24 @@ def test_decode_noalloc_refuses_calls_beyond_its_scratch(lib):
     assert plan.workspace_bytes > _lib.DECODE_NOALLOC_MAX_BYTES
 
 
-def test_plan_flags_reused_context():
-    """Header word 11 (kPAltPrio) is 1 exactly when some sub-sequence has more keys than
-    queries: the paged kernels then alternate wave priorities between steps."""
-    warm = kernels.plan_attention([0, 1183, 1247], [0, 1183, 11924], 16, 2, 128, True, "cpu", num_cus=256)
-    square = kernels.plan_attention([0, 4096], [0, 4096], 16, 2, 128, True, "cpu", num_cus=256)
-    batch = kernels.plan_attention([0, 10, 30, 40], [0, 10, 30, 40], 28, 4, 128, True, "cpu", num_cus=256)
-    one_longer = kernels.plan_attention([0, 10, 30], [0, 10, 31], 28, 4, 128, True, "cpu", num_cus=256)
-    assert [int(p.host[11]) for p in (warm, square, batch, one_longer)] == [1, 0, 0, 1]
+def test_plan_priority_policy():
+    """Header word 11 (kPPrio): 2 (by remaining key tiles) when the plan's items fit in one
+    wave of workgroups (two per CU), else 1 (alternating) when some sub-sequence has more
+    keys than queries (reused context), else 0 (equal)."""
+    def prio(cu_q, cu_k, hq=16, hkv=2):
+        plan = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, True, "cpu", num_cus=256)
+        n_items = int(plan.host[1])
+        return int(plan.host[11]), n_items
+    assert prio([0, 1183, 1247], [0, 1183, 11924]) == (2, 492)           # warm 4K request
+    assert prio([0, 10, 30, 40], [0, 10, 30, 40], 28, 4)[0] == 2          # small square batch
+    assert prio([0, 10, 30], [0, 10, 31], 28, 4)[0] == 2                 # small, reused context
+    p, n = prio([0, 4096], [0, 4096])                                    # dense 4096^2: several waves
+    assert p == 0 and n > 512
+    p, n = prio([0, 10741], [0, 10741])
+    assert p == 0 and n > 512
+    cq, ck = workloads.cfg4().cu_seqlens()                               # 8 requests sharing an image
+    p, n = prio(list(cq), list(ck))
+    assert p == 1 and n > 512
 
 
 def test_paged_attention_refuses_pages_not_multiple_of_16(lib):

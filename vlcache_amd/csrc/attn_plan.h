@@ -33,7 +33,15 @@ enum PlanField {
   kPNumHeadsKv = 8,
   kPCausal = 9,
   kPHeadDim = 10,
-  kPAltPrio = 11,  // 1: some sub-sequence has more keys than queries (reused context)
+  kPPrio = 11,     // wave issue priority: kPrioEqual, kPrioAlternate or kPrioRemaining
+};
+
+// Issue-priority policies of the attention steps (plan field kPPrio).  Two workgroups
+// share each CU; with equal priorities the older one's waves win the issue arbitration.
+enum PrioMode {
+  kPrioEqual = 0,      // equal priorities
+  kPrioAlternate = 1,  // 0 and 2 on the two steps of each pair (their steps are not in phase)
+  kPrioRemaining = 2,  // by the item's remaining key tiles: a workgroup that falls behind catches up
 };
 
 // Work item (int32 x 16): one workgroup.

@@ -67,7 +67,7 @@ struct Params {
   int page_size;
   int group;
   int causal;
-  int alt_prio;  // the plan's kPAltPrio
+  int prio_mode;  // the plan's kPPrio
   float scale_log2;
 };
 
@@ -550,36 +550,38 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     sync_tiles();  // K buffer 0 is reloaded during step 0
 
     // ---- steps: unmasked pairs, masked pairs, a masked single step if n is odd ---
-    // Paged calls over reused context (the plan's kPAltPrio: some sub-sequence has more
-    // keys than queries) alternate the waves' issue priority between the two steps of a
-    // pair.  Two workgroups share each CU; with equal priorities the older one's waves
-    // win the issue arbitration, and in the warm request's call the second workgroup of
-    // a CU progressed at about half the first's rate and finished ≈ 5 us after it.  The
-    // two workgroups' steps are not in phase, so alternating priorities shares the CU
-    // more evenly: 8 requests sharing an image 169.5 against 177.3 us, the 4K warm
-    // request 29.1 against 29.7 us, the two-image 7B batch 113.3 against 114.8 us (same
-    // process, identical results).  Square causal calls, paged or contiguous, measured
-    // slower with it (paged 10741^2 481.3 against 467.6 us, 4096^2 92.0 against 88.7 us)
-    // and keep equal priorities.
-    const bool alt_prio = MODE != kContiguous && p.alt_prio;
-    auto prio = [&](auto high) __attribute__((always_inline)) {
-      if constexpr (MODE != kContiguous)
-        if (alt_prio) __builtin_amdgcn_s_setprio(decltype(high)::value ? 2 : 0);
+    // Issue priority per the plan (kPPrio).  Alternating (0 and 2 on the two steps of a
+    // pair) applies to paged calls only: 8 requests sharing an image 169.5 against 177.3
+    // us with equal priorities, the two-image 7B batch 113.3 against 114.8 us; square
+    // causal calls, paged or contiguous, measured slower with it (paged 10741^2 481.3
+    // against 467.6 us) and the planner leaves them at equal priorities.  By remaining
+    // tiles: 3 for six or more, 2 for four or five, 1 for two or three, 0 for the last.
+    const int prio_mode = p.prio_mode;
+    auto prio = [&](int t, auto high) __attribute__((always_inline)) {
+      if (prio_mode == kPrioRemaining) {
+        const int r = n_tiles - t;
+        if (r >= 6) __builtin_amdgcn_s_setprio(3);
+        else if (r >= 4) __builtin_amdgcn_s_setprio(2);
+        else if (r >= 2) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      } else if constexpr (MODE != kContiguous) {
+        if (prio_mode == kPrioAlternate) __builtin_amdgcn_s_setprio(decltype(high)::value ? 2 : 0);
+      }
     };
     int t = 0;
     for (; t + 1 < n_plain; t += 2) {
-      prio(std::false_type{});
+      prio(t, std::false_type{});
       step(I0{}, Plain{}, t);
-      prio(std::true_type{});
+      prio(t + 1, std::true_type{});
       step(I1{}, Plain{}, t + 1);
     }
     for (; t + 1 < n_tiles; t += 2) {
-      prio(std::false_type{});
+      prio(t, std::false_type{});
       step(I0{}, Masked{}, t);
-      prio(std::true_type{});
+      prio(t + 1, std::true_type{});
       step(I1{}, Masked{}, t + 1);
     }
-    prio(std::false_type{});
+    prio(t, std::false_type{});
     if (t < n_tiles) step(I0{}, Masked{}, t);  // t is even here
     // ---- drain: O^T += V^T P^T of the last tile ---------------------------------------
     if ((n_tiles - 1) & 1) pv_last(v_buf1);
@@ -859,7 +861,7 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
   prm.page_size = block_table ? page_size : 1;
   prm.group = group;
   prm.causal = causal ? 1 : 0;
-  prm.alt_prio = h[kPAltPrio];
+  prm.prio_mode = h[kPPrio];
   prm.scale_log2 = softmax_scale * 1.4426950408889634f;
 
   hipStream_t s = as_stream(stream);
