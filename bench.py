@@ -848,6 +848,10 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(frac, 4),
             "traffic": _profiled_attention_traffic(args.workload),
+            "traffic_source": ("not measured in this run: HBM bytes per call (attn_fwd + attn_combine) from "
+                               "profiles/warm_prefill_3b_4k_r0.1_hbm_traffic.md, rocprofv3 FETCH_SIZE and "
+                               "WRITE_SIZE per dispatch scaled by a plain copy's readings"
+                               if args.workload == "cfg2" else "no traffic profile for this workload"),
         },
         "cpu_baseline": cpu,
         "kernels": {
