@@ -160,8 +160,10 @@ int vlc_attn_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
  *   otherwise; the reference's pages are multiples of 256, config.py:24); key j of
  *   sequence b lives in row
  *   block_table[b*bt_row_stride + j/page_size]*page_size + j%page_size;
- *   k_row_stride/v_row_stride are elements per cache row.  A block id outside
- *   [0, num_blocks) reads as zeros (it is never dereferenced).
+ *   k_row_stride/v_row_stride are elements per cache row.  Row b of the block
+ *   table must hold at least ceil(sk_b / page_size) entries (the kernel reads
+ *   entry j / page_size for every key j < sk_b; the table's width is not passed).
+ *   A block id outside [0, num_blocks) reads as zeros (it is never dereferenced).
  * Contiguous mode (block_table == NULL): key j of sequence b is row
  *   cu_seqlens_k[b] + j of k/v, at k_row_stride / v_row_stride elements.
  * causal: row i of a sequence with lengths (sq, sk) sees keys j <= i + sk - sq
