@@ -242,3 +242,21 @@ def test_rope_cache_matches_engine_rotary_module():
 
     m = MRotaryEmbedding(128, 128, 2048, 1e6, SECTION)
     assert torch.equal(m.cos_sin_cache, orope.rope_cache(2048, 128, 1e6))
+
+
+@pytest.mark.parametrize("deltas,section", [
+    ([[88, 88, 88]], (16, 24, 24)),
+    ([[-5, 3, 7], [48, 48, 48], [0, 0, 0]], (16, 24, 24)),
+    ([12, -7], None),
+    ([[3, 1, 2]], (8, 12, 12)),
+])
+def test_engine_rotation_table_is_the_oracle_table(deltas, section):
+    """The engine's (cos, sin) table (kernels.rerotation_table, per-model constants cached)
+    equals the oracle's bit for bit, before and after the cache is warm."""
+    from vlcache_amd import kernels
+
+    hd = 2 * (sum(section) if section else 64)
+    want = orope.rerotation_cos_sin(deltas, hd, 1e6, None if section is None else list(section))
+    for _ in range(2):
+        got = kernels.rerotation_table(deltas, hd, 1e6, None if section is None else list(section))
+        assert got.dtype == torch.float32 and torch.equal(got, want)

@@ -49,6 +49,32 @@ def _h2d(arr, dtype, device):
     return t.pin_memory().to(device, non_blocking=True)
 
 
+_TORCH_DTYPES = {np.dtype(np.int64): torch.int64, np.dtype(np.int32): torch.int32,
+                 np.dtype(np.float32): torch.float32}
+
+
+def _h2d_many(device, *arrays):
+    """(array, numpy dtype) pairs -> device tensors of the same shapes, sent in ONE copy.
+
+    The arrays are cast and packed at 16-byte aligned offsets into one pinned buffer
+    (torch's pinned-memory cache hands it out again only once its copy has completed),
+    the buffer goes to the device with one non-blocking copy, and each result is a view
+    of the device copy.  A step's index arrays are a few KB to a few hundred KB each: a
+    copy per array costs more host time than the bytes do.
+    """
+    items = [np.ascontiguousarray(a, dtype=dt) for a, dt in arrays]
+    offsets, total = [], 0
+    for a in items:
+        offsets.append(total)
+        total += -(-a.nbytes // 16) * 16
+    host = torch.empty(max(total, 16), dtype=torch.uint8, pin_memory=torch.device(device).type == "cuda")
+    buf = host.numpy()
+    for a, o in zip(items, offsets):
+        buf[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
+    dev = host.to(device, non_blocking=True)
+    return [dev[o:o + a.nbytes].view(_TORCH_DTYPES[a.dtype]).view(a.shape) for a, o in zip(items, offsets)]
+
+
 class ModelRunner:
 
     def __init__(self, config: Config, rank: int = 0, event=None):
@@ -79,6 +105,7 @@ class ModelRunner:
         self.sampler = Sampler()
         self.num_layers = hf.num_hidden_layers
         self.num_kv_heads = hf.num_key_value_heads
+        self.num_cus = torch.cuda.get_device_properties(self.device).multi_processor_count
         self.num_heads = hf.num_attention_heads
         self.head_dim = hf.head_dim
         self._logit_indices = None
@@ -138,17 +165,20 @@ class ModelRunner:
         old = np.asarray(old_slots, dtype=np.int64)
         if old.size == 0:
             return
-        old_t = _h2d(old, torch.int64, self.device)
-        new_t = _h2d(np.asarray(new_slots, dtype=np.int64), torch.int64, self.device)
         rotate = deltas is not None and self.config.rerotate_reused_kv and bool(np.any(np.asarray(deltas)))
-        cos_sin = seg = None
+        arrays = [(old, np.int64), (new_slots, np.int64)]
         if rotate:
             hf = self.config.hf_config
             section = (hf.rope_scaling or {}).get("mrope_section") if self.config.use_mrope else None
-            cos_sin = kernels.rerotation_table(deltas, self.head_dim, hf.rope_theta, section, device=self.device)
+            # (cos, sin) table on the host, sent with the slot lists in one copy
+            arrays.append((kernels.rerotation_table(deltas, self.head_dim, hf.rope_theta, section).numpy(),
+                           np.float32))
             if seg_of_token is not None:
-                seg = _h2d(np.asarray(seg_of_token, dtype=np.int32), torch.int32, self.device)
-        kernels.rerotate_copy_kv(self.kv_cache, old_t, new_t, cos_sin, seg, rotate_k=rotate)
+                arrays.append((seg_of_token, np.int32))
+        dev = _h2d_many(self.device, *arrays)
+        cos_sin = dev[2] if rotate else None
+        seg = dev[3] if rotate and seg_of_token is not None else None
+        kernels.rerotate_copy_kv(self.kv_cache, dev[0], dev[1], cos_sin, seg, rotate_k=rotate)
 
     # ------------------------------------------------------------------ step preparation
     def _checked_ids(self, ids: np.ndarray) -> np.ndarray:
@@ -175,7 +205,6 @@ class ModelRunner:
         has_mm = False
         for seq in seqs:
             n = len(seq)
-            ids = np.asarray(seq.token_ids, dtype=np.int64)
             if seq.mm_inputs:
                 has_mm = True
                 grids = seq.mm_inputs.get("image_grid_thw")
@@ -199,7 +228,7 @@ class ModelRunner:
                 # images: every maximal run of computed tokens, K = everything before its end.
                 runs = seq.computed_runs()
                 for qs, qe in runs:
-                    input_ids.append(ids[qs:qe])
+                    input_ids.append(np.asarray(seq.token_ids[qs:qe], dtype=np.int64))
                     positions.append(self._positions(seq, qs, qe))
                     slot_mapping.append(_slots(seq.block_table, np.arange(qs, qe), self.block_size))
                     cu_q.append(cu_q[-1] + (qe - qs))
@@ -209,7 +238,7 @@ class ModelRunner:
                 logit_indices.append(vidx + len(runs) - 1)
                 vidx += len(runs)
             else:
-                input_ids.append(ids)
+                input_ids.append(np.asarray(seq.token_ids, dtype=np.int64))
                 positions.append(self._positions(seq, 0, n))
                 cu_q.append(cu_q[-1] + n)
                 cu_k.append(cu_k[-1] + n)
@@ -219,20 +248,23 @@ class ModelRunner:
                     vbts.append(seq.block_table)
                 logit_indices.append(vidx)
                 vidx += 1
-        block_tables = None
+        plan_host, ws_bytes = kernels.plan_attention_host(cu_q, cu_k, self.num_heads, self.num_kv_heads,
+                                                          self.head_dim, True, self.num_cus)
+        arrays = [(self._checked_ids(np.concatenate(input_ids)), np.int64),
+                  (np.concatenate(positions, axis=-1), np.int64), (cu_q, np.int32), (cu_k, np.int32),
+                  (np.concatenate(slot_mapping) if slot_mapping else np.zeros(0), np.int32), (plan_host, np.int32)]
         if has_partial and vbts:
             width = max(len(bt) for bt in vbts)
             bt = np.full((len(vbts), width), -1, dtype=np.int32)
             for i, row in enumerate(vbts):
                 bt[i, :len(row)] = row
-            block_tables = _h2d(bt, torch.int32, self.device)
-        input_ids = _h2d(self._checked_ids(np.concatenate(input_ids)), torch.int64, self.device)
-        positions = _h2d(np.concatenate(positions, axis=-1), torch.int64, self.device)
-        cu_q_t = _h2d(np.asarray(cu_q), torch.int32, self.device)
-        cu_k_t = _h2d(np.asarray(cu_k), torch.int32, self.device)
-        slots = _h2d(np.concatenate(slot_mapping) if slot_mapping else np.zeros(0), torch.int32, self.device)
-        plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
-                                      self.device)
+            arrays.append((bt, np.int32))
+        # every input of the step, the attention plan included, in one host-to-device copy
+        dev = _h2d_many(self.device, *arrays)
+        input_ids, positions, cu_q_t, cu_k_t, slots, plan_dev = dev[:6]
+        block_tables = dev[6] if len(dev) > 6 else None
+        plan = kernels.attn_plan_on_device(plan_host, ws_bytes, plan_dev, cu_q, cu_k, self.num_heads,
+                                           self.num_kv_heads, True)
         set_context(True, cu_q_t, cu_k_t, max_q, max_k, slots, None, block_tables, attn_plan=plan,
                     cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
         self._logit_indices = logit_indices if has_partial else None
@@ -267,12 +299,12 @@ class ModelRunner:
         else:
             plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
                                           self.device)
-        set_context(False, _h2d(np.asarray(cu_q), torch.int32, self.device),
-                    _h2d(np.asarray(cu_k), torch.int32, self.device), 1, int(lens.max()),
-                    _h2d(slot, torch.int32, self.device), _h2d(lens, torch.int32, self.device),
-                    _h2d(bt, torch.int32, self.device), attn_plan=plan, cu_seqlens_q_host=cu_q,
-                    cu_seqlens_k_host=cu_k, decode_plan=dplan)
-        return _h2d(input_ids, torch.int64, self.device), _h2d(pos, torch.int64, self.device)
+        cu_q_t, cu_k_t, slot_t, lens_t, bt_t, ids_t, pos_t = _h2d_many(
+            self.device, (cu_q, np.int32), (cu_k, np.int32), (slot, np.int32), (lens, np.int32), (bt, np.int32),
+            (input_ids, np.int64), (pos, np.int64))
+        set_context(False, cu_q_t, cu_k_t, 1, int(lens.max()), slot_t, lens_t, bt_t, attn_plan=plan,
+                    cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k, decode_plan=dplan)
+        return ids_t, pos_t
 
     def _decode_plan(self, batch: int, max_len: int):
         """Decode launch plan for this batch size, sized for contexts up to the next multiple of

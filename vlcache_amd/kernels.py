@@ -6,6 +6,7 @@ the HIP library.  Tensors must live on a HIP device: there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import functools
 from dataclasses import dataclass
 
 import numpy as np
@@ -156,6 +157,20 @@ def rope_store_kvcache(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
 
 
 # --------------------------------------------------------------------------- rerotate
+@functools.lru_cache(maxsize=16)
+def _rotation_pairs(head_dim: int, theta: float, mrope_section: tuple | None):
+    """Section index (long [hd/2]) and fp32 inv_freq of each rotation pair; constants of a
+    model, computed once (read-only: callers index them, never write)."""
+    half = head_dim // 2
+    sec = torch.zeros(half, dtype=torch.long)
+    if mrope_section is not None:
+        if sum(mrope_section) != half:
+            raise ValueError("mrope_section must sum to head_dim / 2")
+        sec = torch.repeat_interleave(torch.arange(3), torch.as_tensor(list(mrope_section)))
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+    return sec, inv
+
+
 def rerotation_table(deltas, head_dim: int, theta: float, mrope_section=None,
                      device=None) -> torch.Tensor:
     """fp32 [num_segments, head_dim/2, 2] (cos, sin) of the per-pair rotation angle.
@@ -170,13 +185,8 @@ def rerotation_table(deltas, head_dim: int, theta: float, mrope_section=None,
     d = torch.as_tensor(np.asarray(deltas), dtype=torch.float64)
     if d.dim() == 1:
         d = d[:, None].expand(-1, 3)
-    half = head_dim // 2
-    sec = torch.zeros(half, dtype=torch.long)
-    if mrope_section is not None:
-        if sum(mrope_section) != half:
-            raise ValueError("mrope_section must sum to head_dim / 2")
-        sec = torch.repeat_interleave(torch.arange(3), torch.as_tensor(list(mrope_section)))
-    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+    sec, inv = _rotation_pairs(head_dim, float(theta),
+                               None if mrope_section is None else tuple(int(x) for x in mrope_section))
     ang = d[:, sec].to(torch.float32) * inv[None, :]
     tab = torch.stack((ang.cos(), ang.sin()), dim=-1).contiguous()
     return tab if device is None else tab.to(device)
@@ -247,17 +257,14 @@ class AttnPlan:
         return int(self.host[3])
 
 
-def plan_attention(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: int,
-                   head_dim: int, causal: bool, device, num_cus: int | None = None) -> AttnPlan:
-    """Build the host work list (vlc_attn_plan) from HOST sequence boundaries."""
+def plan_attention_host(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: int, head_dim: int,
+                        causal: bool, num_cus: int = 256) -> tuple[np.ndarray, int]:
+    """The host work list (vlc_attn_plan) from HOST sequence boundaries: (int32 plan, workspace bytes)."""
     lib = _lib.load()
     cu_q = np.ascontiguousarray(np.asarray(cu_seqlens_q, dtype=np.int32))
     cu_k = np.ascontiguousarray(np.asarray(cu_seqlens_k, dtype=np.int32))
     if cu_q.shape != cu_k.shape or cu_q.ndim != 1 or cu_q.size < 1:
         raise ValueError("cu_seqlens_q/k must be 1-D and of equal length")
-    device = torch.device(device)
-    if num_cus is None:
-        num_cus = _num_cus(device) if device.type == "cuda" else 256
     plan_len = ctypes.c_int64(0)
     ws = ctypes.c_int64(0)
     ip = ctypes.POINTER(ctypes.c_int32)
@@ -270,15 +277,35 @@ def plan_attention(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: i
     st = lib.vlc_attn_plan(*args, host.ctypes.data_as(ip), host.size, ctypes.byref(plan_len),
                            ctypes.byref(ws))
     _lib.check("vlc_attn_plan", st)
+    return host, int(ws.value)
+
+
+def attn_plan_on_device(host: np.ndarray, workspace_bytes: int, dev: torch.Tensor, cu_seqlens_q, cu_seqlens_k,
+                        num_heads_q: int, num_heads_kv: int, causal: bool) -> AttnPlan:
+    """An AttnPlan from a host plan and the caller's device copy of it (int32, same length); allocates
+    the workspace on dev's device."""
+    if dev.dtype != torch.int32 or dev.numel() != host.size or not dev.is_contiguous():
+        raise ValueError("the device plan must be a contiguous int32 copy of the host plan")
+    workspace = (torch.empty(workspace_bytes, dtype=torch.uint8, device=dev.device)
+                 if workspace_bytes > 0 and dev.is_cuda else None)
+    return AttnPlan(host, dev, workspace, len(cu_seqlens_q) - 1, num_heads_q, num_heads_kv, bool(causal),
+                    tuple(int(x) for x in cu_seqlens_q), tuple(int(x) for x in cu_seqlens_k))
+
+
+def plan_attention(cu_seqlens_q, cu_seqlens_k, num_heads_q: int, num_heads_kv: int,
+                   head_dim: int, causal: bool, device, num_cus: int | None = None) -> AttnPlan:
+    """Build the host work list (vlc_attn_plan) from HOST sequence boundaries and copy it to the device."""
+    device = torch.device(device)
+    if num_cus is None:
+        num_cus = _num_cus(device) if device.type == "cuda" else 256
+    host, ws = plan_attention_host(cu_seqlens_q, cu_seqlens_k, num_heads_q, num_heads_kv, head_dim, causal,
+                                   num_cus)
     if device.type == "cuda":
-        pinned = torch.from_numpy(host).pin_memory()
-        dev = pinned.to(device, non_blocking=True)
-        workspace = torch.empty(ws.value, dtype=torch.uint8, device=device) if ws.value > 0 else None
+        dev = torch.from_numpy(host).pin_memory().to(device, non_blocking=True)
     else:
         dev = torch.from_numpy(host.copy())
-        workspace = None
-    return AttnPlan(host, dev, workspace, cu_q.size - 1, num_heads_q, num_heads_kv, bool(causal),
-                    tuple(int(x) for x in cu_q), tuple(int(x) for x in cu_k))
+    return attn_plan_on_device(host, ws, dev, list(np.asarray(cu_seqlens_q).tolist()),
+                               list(np.asarray(cu_seqlens_k).tolist()), num_heads_q, num_heads_kv, causal)
 
 
 def _check_rows(name: str, t: torch.Tensor, heads: int) -> None:
