@@ -430,3 +430,65 @@ def test_image_hash_is_the_reference_digest():
     h2.update(grid.numpy().tobytes())
     h2.update(b.view(torch.int16).numpy().tobytes())
     assert image_hash(b, grid) == h2.intdigest()
+
+
+def test_packed_host_to_device_copy_keeps_every_array():
+    """One buffer, one copy: each array comes back with its values, dtype and shape,
+    at a 16-byte aligned offset, whatever the mix of sizes (empty ones included)."""
+    from vlcache_amd.engine.model_runner import _h2d_many
+
+    rng = np.random.default_rng(3)
+    arrays = [
+        (rng.integers(-2**40, 2**40, 9494), np.int64),
+        (rng.integers(0, 2**31 - 1, (3, 7)), np.int64),
+        (np.array([0, 1183, 1247]), np.int32),
+        (np.zeros(0), np.int32),
+        (np.full((2, 5), -1), np.int32),
+        (rng.standard_normal((1, 64, 2)).astype(np.float32), np.float32),
+        (rng.integers(0, 100, 3), np.int32),
+    ]
+    out = _h2d_many("cpu", *arrays)
+    assert len(out) == len(arrays)
+    base = out[0].untyped_storage().data_ptr()
+    for (a, dt), t in zip(arrays, out):
+        want = np.asarray(a, dtype=dt)
+        assert t.dtype == {np.int64: torch.int64, np.int32: torch.int32, np.float32: torch.float32}[dt]
+        assert tuple(t.shape) == want.shape and t.is_contiguous()
+        assert np.array_equal(t.numpy(), want)
+        assert (t.data_ptr() - base) % 16 == 0
+
+
+def test_registry_releases_least_recently_used_images_when_a_request_does_not_fit():
+    """A request that does not fit the free blocks releases registered images, oldest use
+    first, but never one that a request of the same step copies from."""
+    from vlcache_amd.engine.scheduler import Scheduler
+
+    cfg = Config(dict(QWEN25_VL_3B, image_token_id=IMG), recompute_ratio=0.1, num_kvcache_blocks=8,
+                 max_num_batched_tokens=4096, max_model_len=4096)
+    sch = Scheduler(cfg)
+    sch.image_token_id = IMG
+    bm = sch.block_manager
+    for h in (1, 2):  # two prefilled, finished requests: their images pin 2 blocks each
+        s, _ = _multi([("text", 10), ("image", 500)], [h])
+        bm.allocate(s)
+        s.find_image_token_range(IMG)
+        bm.store_image_kv(s)
+        bm.deallocate(s)
+    assert bm.num_free_blocks == 4
+    probe, _ = _multi([("text", 5), ("image", 500)], [1])
+    assert bm.try_partial_recompute(probe, IMG)  # image 1 is now the most recently used
+    # 1210 tokens need 5 blocks: the least recently used image (2) is released, image 1 stays
+    c, _ = _multi([("text", 10), ("image", 1200)], [3])
+    sch.add(c)
+    seqs, is_prefill = sch.schedule()
+    assert is_prefill and seqs == [c]
+    assert bm.get_image_kv_entry(2) is None and bm.get_image_kv_entry(1) is not None
+    assert bm.num_free_blocks == 1
+    # a request that reuses image 1 needs 2 blocks; the only entry left is the one it copies
+    # from, so nothing is released and it waits (the step decodes c instead)
+    d, _ = _multi([("text", 10), ("image", 500)], [1])
+    sch.add(d)
+    seqs, is_prefill = sch.schedule()
+    assert not is_prefill and seqs == [c]
+    assert bm.get_image_kv_entry(1) is not None and not d.is_partial_recompute
+    assert bm.evict_images(100) == 1 and bm.num_free_blocks == 3 and not bm.image_kv_cache

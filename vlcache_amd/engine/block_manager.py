@@ -13,6 +13,12 @@ the free list is a ring buffer of block ids (a batch of blocks is taken or
 returned with one slice), and decisions are per image, so a prompt may hold
 several images, each reused or computed on its own.  A registry entry also
 records the image's rotary start, which the re-rotation of reused keys needs.
+
+The registry is kept in least-recently-used order (a reuse decision or a store
+touches an entry), and evict_images() releases its oldest entries when a request
+does not fit the pool.  The reference keeps every entry until the same hash is
+stored again, so a stream of distinct images fills its pool with pinned image
+blocks and admission stops for good.
 """
 from __future__ import annotations
 
@@ -122,6 +128,7 @@ class BlockManager:
             entry = self.image_kv_cache.get(span.hash) if span.hash is not None else None
             if entry is not None and entry.img_end - entry.img_start == span.size:
                 span.recompute = math.ceil(self.recompute_ratio * span.size)
+                self.image_kv_cache[span.hash] = self.image_kv_cache.pop(span.hash)  # most recently used
         return seq.is_partial_recompute
 
     def get_image_kv_entry(self, image_hash: int) -> ImageKVEntry | None:
@@ -140,7 +147,7 @@ class BlockManager:
                 continue
             pinned = self._image_blocks(seq.block_table, span.start, span.end)
             self.ref_counts[pinned] += 1
-            old = self.image_kv_cache.get(span.hash)
+            old = self.image_kv_cache.pop(span.hash, None)
             self.image_kv_cache[span.hash] = ImageKVEntry(list(seq.block_table), span.start, span.end,
                                                           span.rope_start)
             if old is not None:
@@ -148,6 +155,21 @@ class BlockManager:
 
     def _unpin(self, entry: ImageKVEntry) -> None:
         self._unref(self._image_blocks(entry.block_table, entry.img_start, entry.img_end))
+
+    def evict_images(self, need_free: int, keep=()) -> int:
+        """Release registry entries, least recently used first and skipping the hashes in
+        keep, until need_free blocks are free or no entry is left to release; returns how
+        many were released.  A released entry's blocks stay with any sequence that still
+        holds them."""
+        released = 0
+        for h in list(self.image_kv_cache):
+            if self._nfree >= need_free:
+                break
+            if h in keep:
+                continue
+            self.release_image(h)
+            released += 1
+        return released
 
     def release_image(self, image_hash: int) -> bool:
         """Drop a registry entry and unpin its blocks; False when the hash is unknown."""

@@ -13,7 +13,10 @@ preempts itself.
 
 Structure: admission and decode planning are separate functions; a decode step
 whose block demand fits the free pool (the usual case) is planned in one pass
-without the per-request preemption loop.
+without the per-request preemption loop.  One addition to the policy: when a
+request does not fit the free blocks, registered image KV that no request of
+the step reuses is released (least recently used first) before admission gives
+up; the reference never releases it, and its pool fills with image blocks.
 """
 from __future__ import annotations
 
@@ -60,6 +63,10 @@ class Scheduler:
             seq = self.waiting[0]
             bm.try_partial_recompute(seq, self.image_token_id)
             cost = seq.prefill_cost
+            if cost <= budget and not bm.can_allocate(seq):
+                # registered images this step copies from stay; older ones make room
+                keep = {sp.hash for s in (*admitted, seq) for sp in s.images if sp.reused > 0}
+                bm.evict_images(seq.num_blocks, keep)
             if cost > budget or not bm.can_allocate(seq):
                 seq.reset_partial_recompute()
                 break
