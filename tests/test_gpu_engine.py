@@ -175,6 +175,32 @@ def test_warm_request_rerotates_reused_keys_to_new_positions(dev):
     assert (kw - kf).abs().max() < 0.5 * (stale - kf).abs().max()
 
 
+def test_registry_releases_old_images_when_the_pool_is_full(dev):
+    say("engine: 8 distinct images through a 6-block pool; registry released oldest first; warm and cold decisions")
+    eng = _engine(0.25, blocks=6)
+    sp = SamplingParams(temperature=1.0, max_tokens=1)
+    grid = (1, 20, 24)  # 120 image tokens: each request fits one block, its image pins it
+
+    def req(img, seed):
+        toks, mm = _request(40, grid, 12, seed)
+        mm["pixel_values"] = mm["pixel_values"] + img  # a distinct image, a distinct hash
+        return toks, mm
+
+    def run(toks, mm):
+        seq = eng.add_request(toks, sp, mm)
+        while not eng.is_finished():
+            eng.step()
+        return seq
+
+    for img in range(8):
+        assert not run(*req(img, seed=img)).is_partial_recompute
+    bm = eng.scheduler.block_manager
+    assert len(bm.image_kv_cache) == 6 and bm.num_free_blocks == 0  # images 0 and 1 were released
+    assert run(*req(7, seed=100)).is_partial_recompute      # the most recent image is reused
+    assert not run(*req(0, seed=101)).is_partial_recompute  # a released image is computed in full
+    assert len(bm.image_kv_cache) == 6
+
+
 def test_model_runner_copy_image_kv_plain_and_rotated(dev):
     say("runner: copy_image_kv without deltas (bit copy) and with deltas (re-rotation)")
     eng = _engine(0.1, blocks=8)
