@@ -485,6 +485,41 @@ def test_attention_random_shapes(dev, seed):
     assert_attn_close(out, ref, what=f"random attention seed {seed}")
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_attention_random_wide(dev, seed):
+    """A wider random space: up to 5 sequences of up to 1300 queries and 4300 keys, page sizes
+    16-256 (page boundaries inside tiles included), contiguous K/V, 16:1 and 1:1 head
+    groupings, plans without splits (num_cus < 0) and with many (num_cus 4096)."""
+    r = np.random.default_rng(50000 + seed)
+    n = int(r.integers(1, 6))
+    subs = []
+    for _ in range(n):
+        sq = int(r.choice([0, 1, int(r.integers(2, 300)), int(r.integers(300, 1300))]))
+        sk = sq + int(r.integers(0, 3000)) if r.random() < 0.85 else max(0, sq - int(r.integers(1, 40)))
+        subs.append((sq, sk))
+    hq, hkv = [(16, 2), (28, 4), (8, 1), (32, 2), (12, 12), (16, 1), (4, 4)][int(r.integers(0, 7))]
+    contiguous = r.random() < 0.2
+    page = int(r.choice([16, 32, 48, 64, 80, 128, 256]))
+    causal = bool(r.random() < 0.7)
+    num_cus = [None, 8, 300, 4096, -1][int(r.integers(0, 5))]
+    say(f"attention wide seed={seed}: subs={subs} heads={hq}/{hkv} page={'contiguous' if contiguous else page} "
+        f"causal={causal} num_cus={num_cus}")
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(70000 + seed, hq, hkv, subs, page=page)
+    if contiguous:
+        rows = [bt[b, j // page].item() * page + j % page for b, (_, sk) in enumerate(subs) for j in range(sk)]
+        k = torch.cat([kc.view(-1, hkv, 128)[rows], torch.zeros(1, hkv, 128, dtype=torch.bfloat16)])
+        v = torch.cat([vc.view(-1, hkv, 128)[rows], torch.zeros(1, hkv, 128, dtype=torch.bfloat16)])
+        plan = kernels.plan_attention(cu_q, cu_k, hq, hkv, 128, causal, dev, num_cus=num_cus)
+        out = kernels.varlen_attention(q.to(dev), k.to(dev), v.to(dev),
+                                       torch.tensor(cu_q, dtype=torch.int32, device=dev),
+                                       torch.tensor(cu_k, dtype=torch.int32, device=dev), 128 ** -0.5, causal,
+                                       None, plan=plan).cpu()
+    else:
+        out, _ = _run_paged(dev, q, kc, vc, bt, cu_q, cu_k, hq, hkv, causal=causal, num_cus=num_cus)
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, causal, bt.tolist(), page)
+    assert_attn_close(out, ref, what=f"wide random attention seed {seed}")
+
+
 @pytest.mark.parametrize("page", [16, 32, 48, 80])
 def test_attention_small_pages_and_non_causal(dev, page):
     """Pages that are multiples of 16 but not of 64: each wave's 16 rows of a tile lie in
@@ -625,6 +660,20 @@ def test_decode_random_shapes(dev, seed):
     splits = [0, 1, int(r.integers(2, 40))][int(r.integers(0, 3))]
     say(f"decode random seed={seed}: lens={lens} heads={hq}/{hkv} page={page} splits={splits}")
     _decode_case(dev, lens, hq, hkv, seed=400 + seed, page=page, num_splits=splits)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_decode_random_wide(dev, seed):
+    """Up to 8 sequences of up to 9000 tokens, 16:1 and 1:1 head groupings, pages 16-256 and
+    forced split counts up to 63."""
+    r = np.random.default_rng(60000 + seed)
+    B = int(r.integers(1, 9))
+    lens = [int(x) for x in r.integers(1, 9000, B)]
+    hq, hkv = [(16, 2), (28, 4), (8, 1), (32, 2), (12, 12), (16, 1)][int(r.integers(0, 6))]
+    page = int(r.choice([16, 32, 64, 128, 256]))
+    splits = [0, 1, int(r.integers(2, 64))][int(r.integers(0, 3))]
+    say(f"decode wide seed={seed}: lens={lens} heads={hq}/{hkv} page={page} splits={splits}")
+    _decode_case(dev, lens, hq, hkv, seed=80000 + seed, page=page, num_splits=splits)
 
 
 @pytest.mark.parametrize("splits", [1, 3, 32])
