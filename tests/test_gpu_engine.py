@@ -371,9 +371,10 @@ def test_decode_graph_replays_match_the_eager_decode(dev):
     """enforce_eager=False: decode steps replay captured HIP graphs.  Three requests (one
     with an image, one long enough to span blocks) are prefilled, then for 5 decode steps
     the eager decode forward and the graph replay (batch 3 padded to the captured size 4)
-    are run on the same step; the logits agree under the cosine bar (the GEMMs of a
-    4-row and a 3-row batch may round differently, and the graph's decode plan covers
-    max_model_len), every replay after eager work and synchronisation.  The batch shrinks
+    are run on the same step; the logits agree under the cosine bar (the graph's decode plan
+    covers max_model_len, the eager step's plan its own context, so their split-KV merges
+    differ; with one plan they are bit-identical, the next test), every replay after eager
+    work and synchronisation.  The batch shrinks
     3 -> 2 -> 1 as requests finish, so three captured sizes (4, 2, 1) replay."""
     from vlcache_amd import LLM
     from vlcache_amd.utils.context import reset_context
@@ -411,6 +412,43 @@ def test_decode_graph_replays_match_the_eager_decode(dev):
         eng.scheduler.postprocess(seqs, le.argmax(-1).tolist())
     assert seen == {1, 2, 3}, seen
     assert set(runner._graphs) == {1, 2, 4}
+
+
+def test_decode_graph_equals_eager_decode_with_its_launch_plan(dev):
+    """The graph replay is the eager decode forward, bit for bit, once the eager step uses the
+    graph's decode launch plan (sized for max_model_len; the eager step's own plan is sized
+    for its context, which changes the split-KV merge order).  Batch 3 replays the graph
+    captured for 4 (a padding row)."""
+    from vlcache_amd import LLM
+    from vlcache_amd.utils.context import reset_context
+
+    say("engine: decode graph replay vs eager decode with the graph's plan, bit for bit")
+    eng = LLM(dict(TINY), recompute_ratio=0.1, num_kvcache_blocks=16, max_model_len=2048, seed=7,
+              synthetic_vision=True, enforce_eager=False, max_num_seqs=8)
+    runner = eng.model_runner
+    plan_for = runner._decode_plan
+    runner._decode_plan = lambda batch, max_len: plan_for(batch, runner.config.max_model_len)
+    rng = np.random.default_rng(2)
+    toks_img, mm = _request(20, (1, 8, 8), 12, 5)
+    prompts = [toks_img, [int(x) for x in rng.integers(1, 900, 300)], [int(x) for x in rng.integers(1, 900, 40)]]
+    for p, m in zip(prompts, [mm, None, None]):
+        eng.add_request(p, SamplingParams(temperature=1.0, max_tokens=4, ignore_eos=True), m)
+    seqs, is_prefill = eng.scheduler.schedule()
+    assert is_prefill
+    eng.scheduler.postprocess(seqs, runner.run(seqs, True)[0])
+    for step in range(3):
+        seqs, is_prefill = eng.scheduler.schedule()
+        assert not is_prefill and len(seqs) == 3
+        with torch.inference_mode():
+            ids, pos = runner.prepare_decode(seqs)
+            le = runner.run_model(ids, pos, False)[0].float().cpu()
+            reset_context()
+            torch.cuda.synchronize()
+            lg = runner._run_decode_graph(seqs).float().cpu()
+            reset_context()
+        assert torch.equal(lg, le), f"decode step {step}: max diff {(lg - le).abs().max().item()}"
+        eng.scheduler.postprocess(seqs, le.argmax(-1).tolist())
+    assert 4 in runner._graphs
 
 
 def test_decode_graph_capture_leaves_other_requests_kv_alone(dev):
