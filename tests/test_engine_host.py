@@ -492,3 +492,17 @@ def test_registry_releases_least_recently_used_images_when_a_request_does_not_fi
     assert not is_prefill and seqs == [c]
     assert bm.get_image_kv_entry(1) is not None and not d.is_partial_recompute
     assert bm.evict_images(100) == 1 and bm.num_free_blocks == 3 and not bm.image_kv_cache
+
+
+def test_visual_rows_count_is_checked_on_the_host():
+    """With image_rows the model places the visual embeddings with index_copy_ (no
+    device-to-host sync); a count mismatch raises before any kernel runs."""
+    from vlcache_amd.qwen_vl import Qwen2_5_VLForConditionalGeneration
+
+    tiny = dict(hidden_size=64, intermediate_size=128, num_hidden_layers=1, num_attention_heads=4,
+                num_key_value_heads=2, vocab_size=100, rms_norm_eps=1e-6, rope_theta=1e6, head_dim=16,
+                max_position_embeddings=256, tie_word_embeddings=True, image_token_id=7, torch_dtype="float32")
+    model = Qwen2_5_VLForConditionalGeneration(load_model_config(tiny))
+    ids = torch.tensor([1, 7, 7, 2])
+    with pytest.raises(ValueError, match="2 image tokens, 3 visual rows"):
+        model(ids, torch.arange(4), torch.zeros(3, 64), torch.tensor([1, 2]))

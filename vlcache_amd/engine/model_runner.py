@@ -250,9 +250,12 @@ class ModelRunner:
                 vidx += 1
         plan_host, ws_bytes = kernels.plan_attention_host(cu_q, cu_k, self.num_heads, self.num_kv_heads,
                                                           self.head_dim, True, self.num_cus)
-        arrays = [(self._checked_ids(np.concatenate(input_ids)), np.int64),
+        ids = self._checked_ids(np.concatenate(input_ids))
+        arrays = [(ids, np.int64),
                   (np.concatenate(positions, axis=-1), np.int64), (cu_q, np.int32), (cu_k, np.int32),
                   (np.concatenate(slot_mapping) if slot_mapping else np.zeros(0), np.int32), (plan_host, np.int32)]
+        if has_mm:  # where the visual rows go, known here on the host
+            arrays.append((np.flatnonzero(ids == self.config.hf_config.image_token_id), np.int64))
         if has_partial and vbts:
             width = max(len(bt) for bt in vbts)
             bt = np.full((len(vbts), width), -1, dtype=np.int32)
@@ -262,7 +265,9 @@ class ModelRunner:
         # every input of the step, the attention plan included, in one host-to-device copy
         dev = _h2d_many(self.device, *arrays)
         input_ids, positions, cu_q_t, cu_k_t, slots, plan_dev = dev[:6]
-        block_tables = dev[6] if len(dev) > 6 else None
+        if has_mm:
+            mm["image_rows"] = dev[6]
+        block_tables = dev[-1] if has_partial and vbts else None
         plan = kernels.attn_plan_on_device(plan_host, ws_bytes, plan_dev, cu_q, cu_k, self.num_heads,
                                            self.num_kv_heads, True)
         set_context(True, cu_q_t, cu_k_t, max_q, max_k, slots, None, block_tables, attn_plan=plan,
@@ -529,7 +534,8 @@ class ModelRunner:
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_prefill, mm=None):
         visual, vit_time = self._process_visual(mm) if (is_prefill and mm) else (None, 0.0)
-        hidden = self.model(input_ids, positions, visual)
+        rows = mm.get("image_rows") if (visual is not None and mm) else None
+        hidden = self.model(input_ids, positions, visual, rows)
         return self.model.compute_logits(hidden), vit_time
 
     @torch.inference_mode()

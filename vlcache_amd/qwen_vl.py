@@ -130,13 +130,21 @@ class Qwen2_5_VLForConditionalGeneration(nn.Module):
             raise RuntimeError("the model config has no vision_config: there is no vision tower")
         return self.visual(pixel_values, grid_thw)
 
-    def forward(self, input_ids, positions, visual_embeds=None):
+    def forward(self, input_ids, positions, visual_embeds=None, image_rows=None):
+        """image_rows: int64 device indices of the image tokens in input_ids, when the caller
+        knows them (the engine does, from its host copy of the ids): the visual rows are then
+        placed without the device-to-host synchronisation that a boolean mask costs."""
         inputs_embeds = self.model.embed_tokens(input_ids)
         if visual_embeds is not None:
-            mask = input_ids == getattr(self.config, "image_token_id", IMAGE_TOKEN_ID)
-            # The reference asserts the count here (a device-to-host sync); a
-            # mismatch raises inside the masked assignment instead.
-            inputs_embeds[mask] = visual_embeds.to(inputs_embeds.dtype)
+            if image_rows is not None:
+                if image_rows.numel() != visual_embeds.shape[0]:
+                    raise ValueError(f"{image_rows.numel()} image tokens, {visual_embeds.shape[0]} visual rows")
+                inputs_embeds.index_copy_(0, image_rows, visual_embeds.to(inputs_embeds.dtype))
+            else:
+                mask = input_ids == getattr(self.config, "image_token_id", IMAGE_TOKEN_ID)
+                # The reference asserts the count here (a device-to-host sync); a
+                # mismatch raises inside the masked assignment instead.
+                inputs_embeds[mask] = visual_embeds.to(inputs_embeds.dtype)
         return self.model(input_ids, positions, inputs_embeds=inputs_embeds)
 
     def compute_logits(self, hidden_states):
