@@ -108,7 +108,8 @@ class ModelRunner:
         self.num_cus = torch.cuda.get_device_properties(self.device).multi_processor_count
         self.num_heads = hf.num_attention_heads
         self.head_dim = hf.head_dim
-        self._logit_indices = None
+        self._logit_indices = None  # host list of the kept logit rows (partial steps)
+        self._logit_rows = None     # the same rows on the device
         self._decode_plans: dict = {}
         self._decode_workspace = None
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
@@ -251,28 +252,31 @@ class ModelRunner:
         plan_host, ws_bytes = kernels.plan_attention_host(cu_q, cu_k, self.num_heads, self.num_kv_heads,
                                                           self.head_dim, True, self.num_cus)
         ids = self._checked_ids(np.concatenate(input_ids))
-        arrays = [(ids, np.int64),
-                  (np.concatenate(positions, axis=-1), np.int64), (cu_q, np.int32), (cu_k, np.int32),
-                  (np.concatenate(slot_mapping) if slot_mapping else np.zeros(0), np.int32), (plan_host, np.int32)]
+        host = {"input_ids": (ids, np.int64), "positions": (np.concatenate(positions, axis=-1), np.int64),
+                "cu_q": (cu_q, np.int32), "cu_k": (cu_k, np.int32),
+                "slots": (np.concatenate(slot_mapping) if slot_mapping else np.zeros(0), np.int32),
+                "plan": (plan_host, np.int32)}
         if has_mm:  # where the visual rows go, known here on the host
-            arrays.append((np.flatnonzero(ids == self.config.hf_config.image_token_id), np.int64))
+            host["image_rows"] = (np.flatnonzero(ids == self.config.hf_config.image_token_id), np.int64)
+        if has_partial:  # the rows whose logits are kept
+            host["logit_rows"] = (logit_indices, np.int64)
         if has_partial and vbts:
             width = max(len(bt) for bt in vbts)
             bt = np.full((len(vbts), width), -1, dtype=np.int32)
             for i, row in enumerate(vbts):
                 bt[i, :len(row)] = row
-            arrays.append((bt, np.int32))
+            host["block_tables"] = (bt, np.int32)
         # every input of the step, the attention plan included, in one host-to-device copy
-        dev = _h2d_many(self.device, *arrays)
-        input_ids, positions, cu_q_t, cu_k_t, slots, plan_dev = dev[:6]
+        dev = dict(zip(host, _h2d_many(self.device, *host.values())))
         if has_mm:
-            mm["image_rows"] = dev[6]
-        block_tables = dev[-1] if has_partial and vbts else None
-        plan = kernels.attn_plan_on_device(plan_host, ws_bytes, plan_dev, cu_q, cu_k, self.num_heads,
+            mm["image_rows"] = dev["image_rows"]
+        plan = kernels.attn_plan_on_device(plan_host, ws_bytes, dev["plan"], cu_q, cu_k, self.num_heads,
                                            self.num_kv_heads, True)
-        set_context(True, cu_q_t, cu_k_t, max_q, max_k, slots, None, block_tables, attn_plan=plan,
-                    cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
+        set_context(True, dev["cu_q"], dev["cu_k"], max_q, max_k, dev["slots"], None, dev.get("block_tables"),
+                    attn_plan=plan, cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
         self._logit_indices = logit_indices if has_partial else None
+        self._logit_rows = dev.get("logit_rows")
+        input_ids, positions = dev["input_ids"], dev["positions"]
         return input_ids, positions, (mm if has_mm else None)
 
     def _decode_host_arrays(self, seqs: list[Sequence]):
@@ -553,8 +557,8 @@ class ModelRunner:
             mm = None
         temperatures = self.prepare_sample(seqs)
         logits, vit_time = self.run_model(input_ids, positions, is_prefill, mm)
-        if is_prefill and self._logit_indices is not None:
-            logits = logits[self._logit_indices]
+        if is_prefill and self._logit_rows is not None:
+            logits = logits.index_select(0, self._logit_rows)  # device indices: no sync
         token_ids = self.sampler(logits, temperatures).tolist()
         reset_context()
         return token_ids, vit_time
