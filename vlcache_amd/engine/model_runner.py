@@ -110,6 +110,7 @@ class ModelRunner:
         self.head_dim = hf.head_dim
         self._logit_indices = None  # host list of the kept logit rows (partial steps)
         self._logit_rows = None     # the same rows on the device
+        self._staged_temperatures = None  # the step's temperatures, sent with its other inputs
         self._decode_plans: dict = {}
         self._decode_workspace = None
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
@@ -260,6 +261,7 @@ class ModelRunner:
             host["image_rows"] = (np.flatnonzero(ids == self.config.hf_config.image_token_id), np.int64)
         if has_partial:  # the rows whose logits are kept
             host["logit_rows"] = (logit_indices, np.int64)
+        host["temperatures"] = ([s.temperature for s in seqs], np.float32)
         if has_partial and vbts:
             width = max(len(bt) for bt in vbts)
             bt = np.full((len(vbts), width), -1, dtype=np.int32)
@@ -276,6 +278,7 @@ class ModelRunner:
                     attn_plan=plan, cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
         self._logit_indices = logit_indices if has_partial else None
         self._logit_rows = dev.get("logit_rows")
+        self._staged_temperatures = dev["temperatures"]
         input_ids, positions = dev["input_ids"], dev["positions"]
         return input_ids, positions, (mm if has_mm else None)
 
@@ -308,9 +311,9 @@ class ModelRunner:
         else:
             plan = kernels.plan_attention(cu_q, cu_k, self.num_heads, self.num_kv_heads, self.head_dim, True,
                                           self.device)
-        cu_q_t, cu_k_t, slot_t, lens_t, bt_t, ids_t, pos_t = _h2d_many(
+        cu_q_t, cu_k_t, slot_t, lens_t, bt_t, ids_t, pos_t, self._staged_temperatures = _h2d_many(
             self.device, (cu_q, np.int32), (cu_k, np.int32), (slot, np.int32), (lens, np.int32), (bt, np.int32),
-            (input_ids, np.int64), (pos, np.int64))
+            (input_ids, np.int64), (pos, np.int64), ([s.temperature for s in seqs], np.float32))
         set_context(False, cu_q_t, cu_k_t, 1, int(lens.max()), slot_t, lens_t, bt_t, attn_plan=plan,
                     cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k, decode_plan=dplan)
         return ids_t, pos_t
@@ -555,7 +558,8 @@ class ModelRunner:
         else:
             input_ids, positions = self.prepare_decode(seqs)
             mm = None
-        temperatures = self.prepare_sample(seqs)
+        # prepare_prefill/prepare_decode sent the temperatures with the step's other inputs
+        temperatures, self._staged_temperatures = self._staged_temperatures, None
         logits, vit_time = self.run_model(input_ids, positions, is_prefill, mm)
         if is_prefill and self._logit_rows is not None:
             logits = logits.index_select(0, self._logit_rows)  # device indices: no sync

@@ -182,12 +182,13 @@ def rerotation_table(deltas, head_dim: int, theta: float, mrope_section=None,
     mrope_section (e.g. [16, 24, 24]: t for i < 16, h for i < 40, w after),
     or the t delta for every pair when mrope_section is None.
     """
-    d = torch.as_tensor(np.asarray(deltas), dtype=torch.float64)
-    if d.dim() == 1:
-        d = d[:, None].expand(-1, 3)
+    d = np.asarray(deltas, dtype=np.float64)
+    if d.ndim == 1:
+        d = np.repeat(d[:, None], 3, axis=1)
     sec, inv = _rotation_pairs(head_dim, float(theta),
                                None if mrope_section is None else tuple(int(x) for x in mrope_section))
-    ang = d[:, sec].to(torch.float32) * inv[None, :]
+    # the fp32 angles in numpy (the same IEEE roundings as torch's), cos/sin in torch
+    ang = torch.from_numpy(d[:, sec.numpy()].astype(np.float32) * inv.numpy()[None, :])
     tab = torch.stack((ang.cos(), ang.sin()), dim=-1).contiguous()
     return tab if device is None else tab.to(device)
 
