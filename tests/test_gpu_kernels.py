@@ -534,6 +534,39 @@ def test_attention_small_pages_and_non_causal(dev, page):
         assert_attn_close(out, ref, what=f"page-{page} causal={causal}")
 
 
+@pytest.mark.parametrize("page", [64, 192, 320])
+def test_attention_block_ids_read_ahead(dev, page):
+    """Paged plans of several waves read each step's block ids one step early and carry the
+    tile's row within its page from step to step.  Pages of 64 keys (a new page every tile)
+    and sizes that are multiples of 64 but not powers of two, with splits that start inside
+    a page: against the oracle, and bit-identical to the same plan run by the kernel that
+    reads the block ids in the step (the one-wave kernel, chosen by the plan's priority
+    word 11 = 2)."""
+    say(f"attention: block ids read a step ahead, page size {page}, multi-wave plan (num_cus 48)")
+    subs = [(300, 2900), (64, 1500), (700, 700), (5, 4100)]
+    hq, hkv = 16, 2
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(31 + page, hq, hkv, subs, page=page)
+    host, ws = kernels.plan_attention_host(cu_q, cu_k, hq, hkv, 128, True, num_cus=48)
+    items = host[16:16 + 16 * int(host[1])].reshape(-1, 16)
+    assert int(host[1]) > 2 * 48 and int(host[11]) != 2  # several waves: the read-ahead kernel
+    if page != 64:
+        assert ((items[:, 6] >= 0) & (items[:, 4] % page != 0)).any()  # a split starts inside a page
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
+    ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+    outs = []
+    for prio in (int(host[11]), 2):
+        h = host.copy()
+        h[11] = prio
+        plan = kernels.attn_plan_on_device(h, ws, torch.from_numpy(h).to(dev), cu_q, cu_k, hq, hkv, True)
+        out = kernels.varlen_attention(q.to(dev), kc.to(dev), vc.to(dev), cq, ck, 128 ** -0.5, True, bt.to(dev),
+                                       plan=plan)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1]), "read-ahead and in-step block ids differ"
+    ref = oattn.varlen_attention(q, kc, vc, cu_q, cu_k, 128 ** -0.5, True, bt.tolist(), page)
+    assert_attn_close(outs[0], ref, what=f"page-{page} read-ahead block ids")
+
+
 def test_attention_rows_without_keys_are_zero(dev):
     say("attention: causal with sk < sq: the first sq-sk rows see no key and are zero")
     subs = [(50, 20)]

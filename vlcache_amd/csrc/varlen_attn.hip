@@ -167,8 +167,11 @@ __device__ __forceinline__ float half_wave_max(float x) {
 // rounded up).  Heads are 128-element rows either way; with head_dim 80 (KS 5, MB 3) the
 // products skip dims 80..127 of q and k and 96..127 of v (output dims 96..127 are zero,
 // 80..95 take v's values there).
-template <int MODE, int KS = 8, int MB = 4>
+// AHEAD (kPagedTiles only): read the block ids of a step's tiles one step early; see
+// the launch for where it is used.
+template <int MODE, int KS = 8, int MB = 4, bool AHEAD = false>
 __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const Params p) {
+  constexpr bool kAheadSrc = MODE == kPagedTiles && AHEAD;
   static_assert(KS >= 1 && KS <= 8 && MB >= 1 && MB <= 4 && 2 * MB >= KS, "head_dim <= 128");
   constexpr int NPV = 4 * MB;       // O^T += V^T P^T MFMAs per tile
   constexpr int NQK = 2 * KS;       // S^T = K Q^T MFMAs per tile
@@ -348,6 +351,34 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     const int64_t row0 = (int64_t)blk * p.page_size + (g0 - pg * p.page_size) - 16 * wave;
     return DmaSrc{ok ? colbase + row0 * st : zero, ok ? (uint32_t)(16 * wave + min(15, sk - 1 - g0)) : 0u};
   };
+  // kAheadSrc: the source of a paged tile load split in two, so that a step can read
+  // the block ids of the next step's tiles early and use them a step later: the LDS
+  // read of tile u's block id (a VGPR, uniform), then the source from it.
+  auto tile_blk_raw = [&](int u) __attribute__((always_inline)) {
+    return tile_blk[min(u, max(n_tiles - 1, 0))];
+  };
+  // Branch-free (the address is formed from a clamped block id and then selected): a
+  // branch here would split the step's straight-line code in the middle.  off: the
+  // tile's first row within its page (split boundaries and page sizes are multiples of
+  // 64 keys, so the next tile's offset is this one's + 64, wrapped at the page size).
+  const int64_t kpage = (int64_t)p.page_size * kst, vpage = (int64_t)p.page_size * vst;
+  auto paged_src = [&](int u, int32_t raw, const char* colbase, int64_t st, int64_t page_bytes, uint32_t off)
+      __attribute__((always_inline)) {
+    const int kt = k_begin + u * kTileK;
+    const int32_t blk = __builtin_amdgcn_readfirstlane(raw);
+    const bool ok = u < n_tiles && blk >= 0 && blk < p.num_blocks;
+    const char* base = colbase + (int64_t)(ok ? blk : 0) * page_bytes + (int64_t)off * st;
+    asm volatile("" : "+s"(base));
+    return DmaSrc{ok ? base : zero, ok ? (uint32_t)min(kTileK - 1, sk - 1 - kt) : 0u};
+  };
+  auto next_off = [&](uint32_t off) __attribute__((always_inline)) {
+    off += kTileK;
+    return off >= (uint32_t)p.page_size ? off - (uint32_t)p.page_size : off;
+  };
+  // kAheadSrc: the sources of the current step's tile loads (K tile t + 2, V tile t),
+  // computed during the previous step (the prologue for step 0).
+  DmaSrc dk_cur{zero, 0u}, dv_cur{zero, 0u};
+  uint32_t koff_nx = 0, voff_nx = 0;  // in-page rows of the next step's K tile t + 3 and V tile t + 1
 
   // O^T += V^T P^T of the last tile, reads a few MFMAs ahead (sched groups: 0x008
   // MFMA, 0x100 LDS read).  MFMA j: dim block j % MB, 16-key chunk (j / MB) & 1, key
@@ -393,7 +424,14 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     constexpr bool MASKED = decltype(masked)::value;
     constexpr int kAhead = 3;
     const int kt = k_begin + t * kTileK;
-    const DmaSrc dk = dma_src(t + 2, kcol, kst), dv = dma_src(t, vcol, vst);
+    // kAheadSrc: the sources were computed a step ahead (reading the block ids here
+    // waits for two LDS round trips before the step's first operand read); the next
+    // step's sources are computed in units kRawUnit (block id reads) and kSrcUnit.
+    constexpr int kRawUnit = 8, kSrcUnit = 20;
+    static_assert(!kAheadSrc || kSrcUnit < NU, "the next step's sources are computed inside the step");
+    const DmaSrc dk = kAheadSrc ? dk_cur : dma_src(t + 2, kcol, kst);
+    const DmaSrc dv = kAheadSrc ? dv_cur : dma_src(t, vcol, vst);
+    int32_t raw_k = 0, raw_v = 0;
     const uint32_t lr = opaque(lrow0), lcn = opaque(lchunk0);
     const int rel = min(limit, k_end - 1) - kt - 4 * hf;  // MASKED: keys past rel are masked
 
@@ -462,6 +500,17 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
         const int r = i - 4;
         dma16(dv.base, __umul24(min(lr + 4 * r, dv.last), (uint32_t)vst) + ((lcn ^ (uint32_t)r) << 4),
               lds_u32(v_ld + (16 * wave + 4 * r) * 256));
+      }
+      if constexpr (kAheadSrc) {  // the next step loads K tile t + 3 and V tile t + 1
+        if (i == kRawUnit) {
+          raw_k = tile_blk_raw(t + 3);
+          raw_v = tile_blk_raw(t + 1);
+        } else if (i == kSrcUnit) {
+          dk_cur = paged_src(t + 3, raw_k, kcol, kst, kpage, koff_nx);
+          dv_cur = paged_src(t + 1, raw_v, vcol, vst, vpage, voff_nx);
+          koff_nx = next_off(koff_nx);
+          voff_nx = next_off(voff_nx);
+        }
       }
       if (i < 3) {  // mask and partial max of elements 11i .. 11i+10
 #pragma unroll
@@ -547,6 +596,13 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCU) void attn_fwd_kernel(const 
     sync_tiles();
     qk(k_buf0, s_even);
     order_qk();
+    if constexpr (kAheadSrc) {  // step 0 loads K tile 2 and V tile 0
+      const uint32_t ps = (uint32_t)p.page_size, kb = (uint32_t)k_begin % ps;
+      dk_cur = paged_src(2, tile_blk_raw(2), kcol, kst, kpage, (kb + 2 * kTileK) % ps);
+      dv_cur = paged_src(0, tile_blk_raw(0), vcol, vst, vpage, kb);
+      koff_nx = (kb + 3 * kTileK) % ps;
+      voff_nx = (kb + kTileK) % ps;
+    }
     sync_tiles();  // K buffer 0 is reloaded during step 0
 
     // ---- steps: unmasked pairs, masked pairs, a masked single step if n is odd ---
@@ -871,9 +927,18 @@ VLC_API int vlc_varlen_attn_fwd(const void* q, int64_t q_row_stride, const void*
                        dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
   else if (mode == kContiguous)
     hipLaunchKernelGGL(attn_fwd_kernel<kContiguous>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
-  else if (mode == kPagedTiles)
-    hipLaunchKernelGGL(attn_fwd_kernel<kPagedTiles>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
-  else
+  else if (mode == kPagedTiles) {
+    // Reading block ids a step ahead: paged 10741^2 473.3 against 480.1 us, 8 requests
+    // sharing an image 169.6 against 175.4, the two-image 7B batch 114.6 against 116.5.
+    // One-wave plans (kPrioRemaining: the warm 4K request) read 0.6-0.9 % slower with it,
+    // in runs where a byte-identical copy of a build read 0.3-0.4 % slower than the
+    // original; they keep the in-step reads.
+    if (prm.prio_mode == kPrioRemaining)
+      hipLaunchKernelGGL(attn_fwd_kernel<kPagedTiles>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<kPagedTiles, 8, 4, true>), dim3((unsigned)n_items), dim3(kThreads), 0, s,
+                         prm);
+  } else
     hipLaunchKernelGGL(attn_fwd_kernel<kPagedRows>, dim3((unsigned)n_items), dim3(kThreads), 0, s, prm);
   int st = launch_status();
   if (st != VLC_OK) return st;
